@@ -1,0 +1,284 @@
+"""Benchmark: fused 2D-RoPE attention fwd+bwd on one MI355X.
+
+Workload (BASELINE metric): ViT-B/16 attention, B=256, H=12, H_img=14 + CLS
+(N=197), D=64, bf16, RoPE base 100; q/k/v/dO ~ N(0,1) synthetic.  One step
+= forward + backward through the public API (``sdpa_triton_fa_rope`` then
+``o.backward(dO)``) with inputs already resident in HBM.
+
+Prints one JSON line (the driver's contract) carrying:
+  value          fwd+bwd TFLOP/s (algorithmic 14*B*H*N^2*D per step / wall time)
+  roofline       dominant kernel (the backward kernel): algorithmic bytes per
+                 launch / its average duration from HIP events on the launch
+                 stream, vs 8 TB/s; `traffic` = measured HBM bytes per launch
+                 from the committed rocprofv3 counter summary, if present
+  cpu_baseline   the PyTorch oracle (Python RoPE + torch SDPA, fp32) on the
+                 host CPU over a bounded slice of the same workload
+  torch_rocm     the same oracle on the GPU in bf16 (torch-ROCm SDPA + RoPE)
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "fwd+bwd TFLOP/s at ViT-B/16 (B256 H12 N197 D64 bf16); % of bf16 MFMA peak"
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+
+WORKLOADS = {
+    "vit_b": dict(B=256, H=12, side=14, has_cls=True, D=64, name="vit_b16_attention_fwd_bwd"),
+    "vit_s": dict(B=512, H=6, side=14, has_cls=True, D=64, name="vit_s16_attention_fwd_bwd"),
+    "vit_l": dict(B=128, H=16, side=16, has_cls=False, D=64, name="vit_l16_256_attention_fwd_bwd"),
+    "hires": dict(B=32, H=12, side=32, has_cls=True, D=128, name="hires_n1025_d128_attention_fwd_bwd"),
+}
+
+
+def flops(B, H, N, D):
+    f = 4.0 * B * H * N * N * D
+    return f, 2.5 * f, 3.5 * f   # fwd, bwd (5 GEMMs), fwd+bwd
+
+
+def hbm_bytes(B, H, N, D, e=2):
+    fwd = 4.0 * B * H * N * D * e + 4.0 * B * H * N
+    bwd = 8.0 * B * H * N * D * e + 4.0 * B * H * N
+    return fwd, bwd
+
+
+def roofline_time(B, H, N, D):
+    ff, fb, _ = flops(B, H, N, D)
+    bf, bb = hbm_bytes(B, H, N, D)
+    tf = max(ff / (PEAK_BF16_TFLOPS * 1e12), bf / (PEAK_HBM_GBS * 1e9))
+    tb = max(fb / (PEAK_BF16_TFLOPS * 1e12), bb / (PEAK_HBM_GBS * 1e9))
+    return tf, tb
+
+
+def make_inputs(wl, device, seed=0, dtype=None):
+    import torch
+
+    dtype = dtype or torch.bfloat16
+    N = wl["side"] ** 2 + int(wl["has_cls"])
+    shape = (wl["B"], wl["H"], N, wl["D"])
+    g = torch.Generator().manual_seed(seed)
+    ts = [torch.randn(shape, generator=g) for _ in range(4)]
+    return [t.to(dtype).to(device) for t in ts]
+
+
+def time_cpu_baseline(wl, budget_s=10.0):
+    """Oracle fwd+bwd in fp32 on the host over B_slice batch rows of the workload."""
+    import torch
+    from oracle import torch_ref
+    from triton_fused_rope_flash_attn_amd import build_axial_rope_pairs
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    sub = dict(wl, B=4 if wl["D"] == 64 else 1)
+    q, k, v, do = make_inputs(sub, "cpu", dtype=torch.float32)
+    cosp, sinp = build_axial_rope_pairs(wl["side"], wl["D"], torch.device("cpu"), base=100.0)
+    B, H, N, D = q.shape
+    times = []
+    for i in range(3):
+        torch_ref.forward_backward(q, k, v, do, cosp, sinp, wl["has_cls"])
+    t_start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        torch_ref.forward_backward(q, k, v, do, cosp, sinp, wl["has_cls"])
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s or len(times) >= 200:
+            break
+    med = statistics.median(times)
+    _, _, fall = flops(B, H, N, D)
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for ln in fh:
+                if ln.startswith("model name"):
+                    cpu_model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": fall / med / 1e12,
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (
+            f"oracle (Python 2D RoPE + torch SDPA math, fp32, autograd) fwd+bwd on B={B} of "
+            f"{wl['B']} (planes {B * H} of {wl['B'] * H}), N={N}, D={D}; median of {len(times)} "
+            f"iterations, {med * 1e3:.1f} ms each; CPU: {cpu_model}"
+        ),
+    }
+
+
+def time_torch_rocm(wl, steps, warmup):
+    """Python 2D RoPE (bf16) + torch SDPA (flash/efficient backend) fwd+bwd on the GPU."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    from oracle import torch_ref
+    from triton_fused_rope_flash_attn_amd import CosSinTable
+
+    q, k, v, do = make_inputs(wl, "cuda")
+    table = CosSinTable(100.0, wl["side"], wl["D"], device="cuda")
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+
+    def step():
+        qh = torch_ref.apply_rope(qq, table.COSP, table.SINP, wl["has_cls"])
+        kh = torch_ref.apply_rope(kk, table.COSP, table.SINP, wl["has_cls"])
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            o = F.scaled_dot_product_attention(qh, kh, vv)
+        o.backward(do)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    B, H, N, D = q.shape
+    _, _, fall = flops(B, H, N, D)
+    return {"value": fall / dt / 1e12, "unit": "TFLOP/s", "ms_per_step": dt * 1e3,
+            "what": "Python 2D RoPE (bf16) + F.scaled_dot_product_attention (flash/efficient), fwd+bwd"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="vit_b", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-torch-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py: --gpus {args.gpus} is not supported: this op runs on one GPU (each (b, h) "
+            "plane is independent; a multi-GPU run would only split the batch). Use --gpus 1.",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+
+    import torch
+    from triton_fused_rope_flash_attn_amd import CosSinTable, sdpa_triton_fa_rope
+    from triton_fused_rope_flash_attn_amd import _lib
+
+    wl = WORKLOADS[args.workload]
+    dev = "cuda"
+    q, k, v, do = make_inputs(wl, dev)
+    B, H, N, D = q.shape
+    table = CosSinTable(100.0, wl["side"], wl["D"], device=dev)
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+
+    def step():
+        o = sdpa_triton_fa_rope(qq, kk, vv, table, has_cls=wl["has_cls"])
+        o.backward(do)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+
+    # Per-kernel durations: HIP events on the stream the kernels are launched on.
+    stream = torch.cuda.current_stream()
+    rope = table.packed()
+    scale = 1.0 / math.sqrt(D)
+    n_pos = N - int(wl["has_cls"])
+    o, lse = torch.ops.farope.attn_fwd(q, k, v, rope, n_pos, wl["has_cls"], scale, _lib.BF16)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+           torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for _ in range(3):
+        torch.ops.farope.attn_bwd(do, q, k, v, o, lse, rope, n_pos, wl["has_cls"], scale, _lib.BF16)
+    for a, b, c in ev:
+        a.record(stream)
+        o, lse = torch.ops.farope.attn_fwd(q, k, v, rope, n_pos, wl["has_cls"], scale, _lib.BF16)
+        b.record(stream)
+        torch.ops.farope.attn_bwd(do, q, k, v, o, lse, rope, n_pos, wl["has_cls"], scale, _lib.BF16)
+        c.record(stream)
+    torch.cuda.synchronize()
+    t_fwd = statistics.mean(a.elapsed_time(b) for a, b, c in ev) * 1e-3
+    t_bwd = statistics.mean(b.elapsed_time(c) for a, b, c in ev) * 1e-3
+
+    f_fwd, f_bwd, f_all = flops(B, H, N, D)
+    by_fwd, by_bwd = hbm_bytes(B, H, N, D)
+    tf_star, tb_star = roofline_time(B, H, N, D)
+    desc = _lib.make_desc(B, H, N, D, n_pos, wl["has_cls"], _lib.BF16, _lib.BF16, scale)
+    bwd_cfg = _lib.tile_config(desc, 1)
+    fwd_cfg = _lib.tile_config(desc, 0)
+    bwd_kernel = "bwd_dkdv_kernel<FUSED>" if bwd_cfg[0] == 0 else "bwd_dq_kernel + bwd_dkdv_kernel"
+
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        try:
+            with open(TRAFFIC_FILE) as fh:
+                tr = json.load(fh)
+            traffic = tr.get(args.workload, {}).get("bwd_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+
+    value = f_all / dt / 1e12
+    achieved_gbs = by_bwd / t_bwd / 1e9
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (q, k, v, dO ~ N(0,1), seed 0)",
+        "config": {
+            "workload": wl["name"], "B": B, "H": H, "N": N, "D": D, "H_img": wl["side"],
+            "has_cls": wl["has_cls"], "rope_base": 100.0, "parallelism": "none (1 GPU)",
+        },
+        "pct_mfma_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
+        "roofline_fraction_fwd_bwd": round((tf_star + tb_star) / dt, 4),
+        "fwd": {"ms": round(t_fwd * 1e3, 4), "tflops": round(f_fwd / t_fwd / 1e12, 2),
+                "gbs": round(by_fwd / t_fwd / 1e9, 1), "roofline_fraction": round(tf_star / t_fwd, 4),
+                "tile": fwd_cfg},
+        "bwd": {"ms": round(t_bwd * 1e3, 4), "tflops": round(f_bwd / t_bwd / 1e12, 2),
+                "gbs": round(achieved_gbs, 1), "roofline_fraction": round(tb_star / t_bwd, 4),
+                "tile": bwd_cfg},
+        "roofline": {
+            "kernel": bwd_kernel,
+            "bound": "hbm" if f_bwd / by_bwd < PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9) else "mfma",
+            "achieved": round(achieved_gbs, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved_gbs / PEAK_HBM_GBS, 4),
+            "traffic": traffic,
+        },
+    }
+    if result["roofline"]["bound"] == "mfma":
+        ach = f_bwd / t_bwd / 1e12
+        result["roofline"].update(achieved=round(ach, 1), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
+                                  frac=round(ach / PEAK_BF16_TFLOPS, 4))
+    if not args.no_torch_baseline:
+        try:
+            result["torch_rocm"] = time_torch_rocm(wl, max(5, args.steps // 5), 3)
+        except Exception as exc:  # reported, never fatal for the bench line
+            result["torch_rocm"] = {"error": repr(exc)[:200]}
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = time_cpu_baseline(wl)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,155 @@
+/*
+ * farope: fused 2D axial RoPE + scaled-dot-product attention (forward and
+ * backward) for AMD MI355X (gfx950).  Plain C ABI: device pointers, element
+ * strides and sizes only.  Every entry point enqueues work on `stream` (a
+ * hipStream_t, may be NULL for the default stream), allocates nothing and
+ * returns FAROPE_OK or a farope_status code; argument errors are detected
+ * on the host before anything is launched.
+ *
+ * Reference interface replaced: the Triton launches of
+ * "fa_rope_full .py" (v1kstrand/triton_fused_rope_flash_attn), cited per
+ * function as FA:<line>.
+ *
+ * Tensor conventions: q, k, v, o, dout, dq, dk, dv are [B, H, N, D] with
+ * arbitrary element strides (stride[0..3] = b, h, n, d; stride 0 allowed for
+ * inputs); lse and delta are contiguous fp32 [B*H, N].
+ */
+#ifndef FAROPE_H
+#define FAROPE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FAROPE_ABI_VERSION 1
+
+typedef enum farope_dtype {
+  FAROPE_F32 = 0,
+  FAROPE_F16 = 1,
+  FAROPE_BF16 = 2
+} farope_dtype;
+
+typedef enum farope_status {
+  FAROPE_OK = 0,
+  FAROPE_ERR_NULL = 1,        /* a required pointer is NULL */
+  FAROPE_ERR_HEAD_DIM = 2,    /* head_dim not supported (needs D % 4 == 0; kernels: 64, 128) */
+  FAROPE_ERR_SEQ_LEN = 3,     /* seq_len != n_pos + has_cls, or seq_len < 1 */
+  FAROPE_ERR_DTYPE = 4,       /* unknown io or compute dtype */
+  FAROPE_ERR_TABLE = 5,       /* RoPE table geometry inconsistent with the call */
+  FAROPE_ERR_SHAPE = 6,       /* batch/heads not positive or sizes overflow */
+  FAROPE_ERR_LAUNCH = 7,      /* the HIP runtime rejected a kernel launch */
+  FAROPE_ERR_ALIGN = 8        /* a pointer is not aligned to its element size */
+} farope_status;
+
+/* Problem description shared by all attention entry points. */
+typedef struct farope_attn_desc {
+  int32_t batch;          /* B */
+  int32_t heads;          /* H */
+  int32_t seq_len;        /* N = n_pos + has_cls (FA:1016-1021) */
+  int32_t head_dim;       /* D */
+  int32_t n_pos;          /* rows of the RoPE grid, H_img * H_img */
+  int32_t has_cls;        /* 1: token 0 is a CLS token and bypasses RoPE */
+  int32_t io_dtype;       /* farope_dtype of q, k, v, o, dout, dq, dk, dv */
+  int32_t compute_dtype;  /* farope_dtype the contractions run in (FA:65-73) */
+  float softmax_scale;    /* 1/sqrt(D) in the reference (FA:1024) */
+} farope_attn_desc;
+
+/* ABI version of the loaded library (FAROPE_ABI_VERSION). */
+int farope_abi_version(void);
+
+/* Human-readable text for a farope_status code. */
+const char* farope_strerror(int status);
+
+/* Number of fp32 elements of a packed RoPE table: (n_pos + 1) * d2 * 2. */
+size_t farope_rope_packed_elems(int32_t n_pos, int32_t d2);
+
+/*
+ * Re-lay the pairwise tables COSP/SINP [n_pos, d2] fp32 (any strides) into
+ * the kernels' packed layout [(n_pos + 1), d2, (cos, sin)], row 0 = identity
+ * rotation for the CLS token.  Replaces the per-tile transposed cos/sin
+ * gathers of every reference kernel (FA:182-198, FA:253-269) with one
+ * contiguous 32-byte load per 8 channels.  Tables built by
+ * build_axial_rope_pairs (FA:10-63).
+ */
+int farope_rope_pack(const float* cosp, int64_t cos_stride0, int64_t cos_stride1,
+                     const float* sinp, int64_t sin_stride0, int64_t sin_stride1,
+                     int32_t n_pos, int32_t d2, float* packed, void* stream);
+
+/*
+ * Forward: o = softmax(scale * (R q)(R k)^T) v, lse = logsumexp of the
+ * scaled logits per row (natural log).  Replaces the _attn_fwd launch
+ * (FA:1036-1057; kernel FA:91-315).
+ */
+int farope_attn_fwd(const farope_attn_desc* desc,
+                    const void* q, const int64_t q_stride[4],
+                    const void* k, const int64_t k_stride[4],
+                    const void* v, const int64_t v_stride[4],
+                    const float* rope_packed,
+                    void* o, const int64_t o_stride[4],
+                    float* lse, void* stream);
+
+/* delta = rowsum(dout * o) in fp32.  Replaces _attn_bwd_preprocess
+ * (launch FA:1076-1082; kernel FA:325-357). */
+int farope_attn_bwd_preprocess(const farope_attn_desc* desc,
+                               const void* o, const int64_t o_stride[4],
+                               const void* dout, const int64_t dout_stride[4],
+                               float* delta, void* stream);
+
+/* dk, dv from q, k, v, dout, lse, delta.  Replaces _attn_bwd_dk_dv_rope
+ * (launch FA:1084-1107; kernel FA:374-691). */
+int farope_attn_bwd_dk_dv(const farope_attn_desc* desc,
+                          const void* q, const int64_t q_stride[4],
+                          const void* k, const int64_t k_stride[4],
+                          const void* v, const int64_t v_stride[4],
+                          const void* dout, const int64_t dout_stride[4],
+                          const float* lse, const float* delta,
+                          const float* rope_packed,
+                          void* dk, const int64_t dk_stride[4],
+                          void* dv, const int64_t dv_stride[4], void* stream);
+
+/* dq from q, k, v, dout, lse, delta.  Replaces _attn_bwd_dq_rope
+ * (launch FA:1109-1136; kernel FA:708-1009). */
+int farope_attn_bwd_dq(const farope_attn_desc* desc,
+                       const void* q, const int64_t q_stride[4],
+                       const void* k, const int64_t k_stride[4],
+                       const void* v, const int64_t v_stride[4],
+                       const void* dout, const int64_t dout_stride[4],
+                       const float* lse, const float* delta,
+                       const float* rope_packed,
+                       void* dq, const int64_t dq_stride[4], void* stream);
+
+/*
+ * Whole backward pass (what TritonAttention.backward does, FA:1067-1138):
+ * picks the fused one-launch kernel when the plane fits on chip (D = 64,
+ * N <= 256), else dq (which also writes delta) followed by dk/dv.
+ * delta_ws: caller-owned fp32 workspace of batch*heads*seq_len elements.
+ */
+int farope_attn_bwd(const farope_attn_desc* desc,
+                    const void* q, const int64_t q_stride[4],
+                    const void* k, const int64_t k_stride[4],
+                    const void* v, const int64_t v_stride[4],
+                    const void* o, const int64_t o_stride[4],
+                    const void* dout, const int64_t dout_stride[4],
+                    const float* lse, const float* rope_packed,
+                    void* dq, const int64_t dq_stride[4],
+                    void* dk, const int64_t dk_stride[4],
+                    void* dv, const int64_t dv_stride[4],
+                    float* delta_ws, void* stream);
+
+/*
+ * Tile table query (replaces the reference's triton.autotune configs,
+ * FA:76-90, FA:318-324, FA:359-373, FA:693-707).  which: 0 = forward,
+ * 1 = backward.  out[0] = variant (fwd: 0 plane-resident, 1 streamed;
+ * bwd: 0 fused, 1 split), out[1] = rows per workgroup, out[2] = workgroups
+ * per (b, h) plane, out[3] = threads per workgroup.
+ */
+int farope_tile_config(const farope_attn_desc* desc, int32_t which, int32_t out[4]);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FAROPE_H */

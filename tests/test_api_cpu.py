@@ -1,0 +1,112 @@
+"""Host-side behaviour of the Python API (no GPU needed).
+
+Covers the reference's argument checks and messages (FA:1016-1021), the
+compute-dtype rule (FA:65-73), the no-fallback rule (CPU tensors raise),
+RoPE-table validation, and the custom ops' fake (meta) kernels.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+from torch._subclasses.fake_tensor import FakeTensorMode
+
+from triton_fused_rope_flash_attn_amd import CosSinTable, TritonAttention, _sdpa_comp_dtype, sdpa_triton_fa_rope
+from triton_fused_rope_flash_attn_amd import attention
+
+
+def _qkv(B=2, H=3, N=197, D=64, dtype=torch.bfloat16):
+    return [torch.randn(B, H, N, D).to(dtype) for _ in range(3)]
+
+
+def test_comp_dtype_follows_input_without_autocast():
+    for dt in (torch.float32, torch.float16, torch.bfloat16):
+        assert _sdpa_comp_dtype(torch.zeros(1, dtype=dt)) == dt
+
+
+def test_comp_dtype_follows_autocast(monkeypatch):
+    monkeypatch.setattr(torch, "is_autocast_enabled", lambda *a: True)
+    monkeypatch.setattr(torch, "get_autocast_dtype", lambda dev: torch.bfloat16)
+    assert _sdpa_comp_dtype(torch.zeros(1, dtype=torch.float32)) == torch.bfloat16
+
+
+def test_comp_dtype_rejects_other_dtypes():
+    with pytest.raises(TypeError):
+        _sdpa_comp_dtype(torch.zeros(1, dtype=torch.float64))
+
+
+def test_head_dim_assert_message():
+    q, k, v = _qkv(D=66)
+    table = CosSinTable(100.0, 14, 64, device="cpu")
+    with pytest.raises(AssertionError, match=r"HEAD_DIM must be divisible by 4 \(2D RoPE requires pairs\)\."):
+        TritonAttention.apply(q, k, v, table)
+
+
+def test_seq_len_assert_messages():
+    table = CosSinTable(100.0, 14, 64, device="cpu")
+    q, k, v = _qkv(N=196)
+    with pytest.raises(AssertionError, match=r"SEQ_LEN must be 1 \+ H_img\*W_img when has_cls=True \(got 196 vs 197\)\."):
+        TritonAttention.apply(q, k, v, table)
+    q, k, v = _qkv(N=197)
+    with pytest.raises(AssertionError, match=r"SEQ_LEN must equal H_img\*W_img when has_cls=False \(got 197 vs 196\)\."):
+        TritonAttention.apply(q, k, v, table, 14, False)
+
+
+def test_public_entry_defaults_match_reference():
+    """sdpa_triton_fa_rope(Q, K, V, cos_sin) == TritonAttention.apply(Q, K, V, cos_sin): CLS, H_img 14."""
+    table = CosSinTable(100.0, 14, 64, device="cpu")
+    q, k, v = _qkv(N=196)
+    with pytest.raises(AssertionError, match="got 196 vs 197"):
+        sdpa_triton_fa_rope(q, k, v, table)
+
+
+def test_cpu_tensors_fail_loudly_no_fallback():
+    table = CosSinTable(100.0, 14, 64, device="cpu")
+    q, k, v = _qkv()
+    with pytest.raises(RuntimeError, match="ROCm GPUs only"):
+        sdpa_triton_fa_rope(q, k, v, table)
+    with pytest.raises(RuntimeError, match="ROCm GPUs only"):
+        table.packed()
+
+
+def test_mixed_dtypes_rejected():
+    table = CosSinTable(100.0, 14, 64, device="cpu")
+    q, k, v = _qkv()
+    with pytest.raises(TypeError, match="share one dtype"):
+        sdpa_triton_fa_rope(q, k.float(), v, table)
+
+
+def test_table_shape_is_checked_against_the_call():
+    table = CosSinTable(100.0, 14, 64, device="cpu")
+    with pytest.raises(ValueError, match="does not match the call"):
+        attention.rope_operand(table, 196, 128, torch.device("cpu"))
+    with pytest.raises(ValueError, match="does not match the call"):
+        attention.rope_operand(table, 256, 64, torch.device("cpu"))
+
+
+def test_h_img_inferred_from_square_table_only():
+    class Odd:
+        def tables(self):
+            return torch.zeros(10, 32), torch.zeros(10, 32)
+
+    q, k, v = _qkv(N=11)
+    with pytest.raises(ValueError, match="not a square"):
+        sdpa_triton_fa_rope(q, k, v, Odd())
+
+
+def test_fake_kernels_shapes_and_dtypes():
+    with FakeTensorMode():
+        q = torch.empty(2, 3, 197, 64, dtype=torch.bfloat16, device="cuda")
+        rope = torch.empty(197 * 32 * 2, dtype=torch.float32, device="cuda")
+        o, lse = torch.ops.farope.attn_fwd(q, q, q, rope, 196, True, 0.125, 2)
+        assert o.shape == q.shape and o.dtype == q.dtype
+        assert lse.shape == (2, 3, 197) and lse.dtype == torch.float32
+        dq, dk, dv = torch.ops.farope.attn_bwd(q, q, q, q, o, lse, rope, 196, True, 0.125, 2)
+        for t in (dq, dk, dv):
+            assert t.shape == q.shape and t.dtype == q.dtype
+
+
+def test_custom_ops_registered_with_autograd():
+    assert hasattr(torch.ops.farope, "attn_fwd") and hasattr(torch.ops.farope, "attn_bwd")
+    from torch._library.custom_ops import CustomOpDef
+
+    assert isinstance(attention.attn_fwd, CustomOpDef)

@@ -1,0 +1,268 @@
+"""GPU parity: the HIP kernels (through the C ABI) vs the fp32 PyTorch oracle.
+
+Oracle: Python 2D RoPE + torch SDPA (math backend) in fp32 on the GPU,
+from the same seeded inputs (cast to fp32) and the same CosSinTable.
+Tolerance (north star): O/dQ/dK/dV max_abs_err <= 3e-2 and
+mean_abs_err <= 1e-3 (TOL_MAX / TOL_MEAN in tests/cases.py).
+"""
+from __future__ import annotations
+
+import math
+import sys
+
+import pytest
+import torch
+
+from oracle import torch_ref
+from tests.cases import (CONFIGS, ROPE_BASE, TOL_MAX, TOL_MEAN, allowed, errors, make_inputs,
+                         rounding_floor, seq_len)
+from triton_fused_rope_flash_attn_amd import CosSinTable, TritonAttention, sdpa_triton_fa_rope
+from triton_fused_rope_flash_attn_amd import _lib
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _say(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _run_ours(q, k, v, do, table, has_cls, autocast_dtype=None, sum_loss=False):
+    qq, kk, vv = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    if autocast_dtype is not None:
+        with torch.autocast("cuda", dtype=autocast_dtype):
+            o = sdpa_triton_fa_rope(qq, kk, vv, table, has_cls=has_cls)
+    else:
+        o = sdpa_triton_fa_rope(qq, kk, vv, table, has_cls=has_cls)
+    if sum_loss:
+        o.sum().backward()
+    else:
+        o.backward(do)
+    torch.cuda.synchronize()
+    return o.detach(), qq.grad, kk.grad, vv.grad
+
+
+def _ref(q, k, v, do, table, has_cls):
+    cosp, sinp = table.tables()
+    return torch_ref.forward_backward(q.float(), k.float(), v.float(), do.float(), cosp, sinp, has_cls)
+
+
+def _torch_bf16(q, k, v, do, table, has_cls):
+    """torch-ROCm SDPA + Python RoPE in the input dtype (flash/efficient backends only)."""
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    qq, kk, vv = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    qh = torch_ref.apply_rope(qq, table.COSP, table.SINP, has_cls)
+    kh = torch_ref.apply_rope(kk, table.COSP, table.SINP, has_cls)
+    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        o = F.scaled_dot_product_attention(qh, kh, vv)
+    o.backward(do)
+    torch.cuda.synchronize()
+    return o.detach(), qq.grad, kk.grad, vv.grad
+
+
+def _compare(tag, ours, ref, tol_max=TOL_MAX, tol_mean=TOL_MEAN, out_dtype=None, other=None):
+    """Check max/mean abs error of ours vs ref.
+
+    With out_dtype set, the bound is max(tolerance, FLOOR_MULT x the error of
+    storing ref in out_dtype) (see tests/cases.py).  `other` (torch bf16) is
+    only printed for comparison.
+    """
+    names = ("O", "dQ", "dK", "dV")
+    fails = []
+    for i, (name, a, b) in enumerate(zip(names, ours, ref)):
+        assert a.shape == b.shape, (name, a.shape, b.shape)
+        assert torch.isfinite(a).all(), f"{tag} {name}: non-finite values"
+        mx, mn = errors(a, b)
+        lim_max, lim_mean = tol_max, tol_mean
+        extra = ""
+        if out_dtype is not None and out_dtype != torch.float32:
+            fmx, fmn = rounding_floor(b, out_dtype)
+            lim_max, lim_mean = allowed(fmx, fmn)
+            lim_max, lim_mean = max(lim_max, tol_max), max(lim_mean, tol_mean)
+            extra = f" | storage floor max {fmx:.3e} mean {fmn:.3e}"
+        if other is not None:
+            omx, omn = errors(other[i], b)
+            extra += f" | torch-bf16 max {omx:.3e} mean {omn:.3e}"
+        _say(f"[{tag}] {name}: max_abs_err={mx:.3e} mean_abs_err={mn:.3e} (bound {lim_max:.2e}/{lim_mean:.2e}){extra}")
+        if mx > lim_max or mn > lim_mean:
+            fails.append(f"{name}: max {mx:.3e} (bound {lim_max:.2e}) mean {mn:.3e} (bound {lim_mean:.2e})")
+    assert not fails, f"{tag}: " + "; ".join(fails)
+
+
+@pytest.mark.parametrize("name", ["cpu", "vit_s", "vit_b", "vit_l", "hires"])
+def test_parity_baseline_configs(name):
+    cfg = CONFIGS[name]
+    _say(f"case {name}: {cfg}")
+    q, k, v, do = make_inputs(cfg, DEV)
+    table = CosSinTable(ROPE_BASE, cfg["side"], cfg["D"], device=DEV)
+    ours = _run_ours(q, k, v, do, table, cfg["has_cls"], sum_loss=cfg["dout"] == "ones")
+    ref = _ref(q, k, v, do, table, cfg["has_cls"])
+    other = None
+    if cfg["dtype"] == torch.bfloat16:
+        other = _torch_bf16(q, k, v, do, table, cfg["has_cls"])
+    _compare(name, ours, ref, out_dtype=cfg["dtype"], other=other)
+
+
+def test_lse_matches_logsumexp():
+    cfg = dict(CONFIGS["vit_b"], B=4)
+    q, k, v, _ = make_inputs(cfg, DEV)
+    table = CosSinTable(ROPE_BASE, cfg["side"], cfg["D"], device=DEV)
+    N, D = seq_len(cfg), cfg["D"]
+    o, lse = torch.ops.farope.attn_fwd(q, k, v, table.packed(), N - 1, True, 1 / math.sqrt(D), _lib.BF16)
+    ref = torch_ref.logsumexp_rows(q.float(), k.float(), table.COSP, table.SINP, True)
+    mx, _ = errors(lse, ref)
+    _say(f"[lse] max_abs_err={mx:.3e}")
+    assert mx < 2e-2
+
+
+def test_autocast_fp32_leaves():
+    """README example: fp32 leaves under bf16 autocast -> fp32 O and grads."""
+    cfg = dict(CONFIGS["cpu"], dout="randn")
+    q, k, v, do = make_inputs(cfg, DEV)
+    table = CosSinTable(ROPE_BASE, 14, 64, device=DEV)
+    ours = _run_ours(q, k, v, do, table, True, autocast_dtype=torch.bfloat16)
+    assert ours[0].dtype == torch.float32 and ours[1].dtype == torch.float32
+    ref = _ref(q, k, v, do, table, True)
+    _compare("autocast-bf16", ours, ref)
+
+
+def test_fp16_io():
+    cfg = dict(CONFIGS["vit_b"], B=8, dtype=torch.float16)
+    q, k, v, do = make_inputs(cfg, DEV)
+    table = CosSinTable(ROPE_BASE, 14, 64, device=DEV)
+    ours = _run_ours(q, k, v, do, table, True)
+    ref = _ref(q, k, v, do, table, True)
+    _compare("fp16", ours, ref, out_dtype=torch.float16)
+
+
+def test_fp32_compute_is_tight():
+    """fp32 I/O without autocast computes in fp32 (bf16x3 split products)."""
+    cfg = dict(CONFIGS["cpu"], dout="randn")
+    q, k, v, do = make_inputs(cfg, DEV)
+    table = CosSinTable(ROPE_BASE, 14, 64, device=DEV)
+    ours = _run_ours(q, k, v, do, table, True)
+    ref = _ref(q, k, v, do, table, True)
+    _compare("fp32", ours, ref, tol_max=1e-4, tol_mean=1e-5)
+
+
+@pytest.mark.parametrize(
+    "side,has_cls,D",
+    [(7, True, 64), (5, False, 64), (16, True, 64), (14, True, 128), (3, False, 128), (1, True, 64)],
+)
+def test_ragged_and_variant_shapes(side, has_cls, D):
+    """Ragged N (N % 32 != 0), no-CLS, N > 256 (streamed fwd + split bwd), D=128, N=2."""
+    cfg = dict(B=3, H=5, side=side, has_cls=has_cls, D=D, dtype=torch.bfloat16, scale=1.0, dout="randn")
+    q, k, v, do = make_inputs(cfg, DEV, seed=1)
+    table = CosSinTable(ROPE_BASE, side, D, device=DEV)
+    ours = _run_ours(q, k, v, do, table, has_cls)
+    ref = _ref(q, k, v, do, table, has_cls)
+    _compare(f"side{side}-cls{int(has_cls)}-D{D}", ours, ref, out_dtype=torch.bfloat16)
+
+
+def test_strided_qkv_views():
+    """q/k/v as permuted views of one [B, N, 3, H, D] projection (ViT attention layout)."""
+    B, H, side, D = 4, 12, 14, 64
+    N = side * side + 1
+    g = torch.Generator().manual_seed(3)
+    qkv = torch.randn(B, N, 3, H, D, generator=g).to(torch.bfloat16).to(DEV)
+    q, k, v = qkv.permute(2, 0, 3, 1, 4).unbind(0)
+    assert not q.is_contiguous()
+    do = torch.randn(B, H, N, D, generator=g).to(torch.bfloat16).to(DEV)
+    table = CosSinTable(ROPE_BASE, side, D, device=DEV)
+    ours = _run_ours(q, k, v, do, table, True)
+    ref = _ref(q, k, v, do, table, True)
+    _compare("qkv-views", ours, ref, out_dtype=torch.bfloat16)
+
+
+def test_channel_strided_inputs_generic_path():
+    """d-stride != 1 (generic gather path) gives the same answer."""
+    B, H, side, D = 2, 3, 14, 64
+    N = side * side + 1
+    g = torch.Generator().manual_seed(4)
+    base = [torch.randn(B, H, D, N, generator=g).to(torch.bfloat16).to(DEV) for _ in range(3)]
+    q, k, v = (t.transpose(-1, -2) for t in base)
+    assert q.stride(-1) != 1
+    do = torch.randn(B, H, N, D, generator=g).to(torch.bfloat16).to(DEV)
+    table = CosSinTable(ROPE_BASE, side, D, device=DEV)
+    ours = _run_ours(q, k, v, do, table, True)
+    ref = _ref(q, k, v, do, table, True)
+    _compare("d-strided", ours, ref, out_dtype=torch.bfloat16)
+
+
+def test_stride0_dout_from_sum():
+    cfg = dict(CONFIGS["vit_b"], B=4)
+    q, k, v, _ = make_inputs(cfg, DEV)
+    table = CosSinTable(ROPE_BASE, 14, 64, device=DEV)
+    ours = _run_ours(q, k, v, None, table, True, sum_loss=True)
+    ref = _ref(q, k, v, torch.ones_like(q, dtype=torch.float32), table, True)
+    _compare("stride0-dO", ours, ref, out_dtype=torch.bfloat16)
+
+
+def test_triton_attention_apply_signature():
+    """TritonAttention.apply(Q, K, V, cos_sin, H_img, has_cls) as in the reference."""
+    B, H, side, D = 2, 4, 16, 64
+    cfg = dict(B=B, H=H, side=side, has_cls=False, D=D, dtype=torch.bfloat16, scale=1.0, dout="randn")
+    q, k, v, do = make_inputs(cfg, DEV, seed=5)
+    table = CosSinTable(ROPE_BASE, side, D, device=DEV)
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    o = TritonAttention.apply(qq, kk, vv, table, side, False)
+    o.backward(do)
+    ref = _ref(q, k, v, do, table, False)
+    _compare("TritonAttention.apply", (o.detach(), qq.grad, kk.grad, vv.grad), ref, out_dtype=torch.bfloat16)
+
+
+def test_split_entry_points_match_fused():
+    """preprocess + dk_dv + dq entry points (reference launch structure) == one-call backward."""
+    cfg = dict(CONFIGS["vit_b"], B=4)
+    q, k, v, do = make_inputs(cfg, DEV)
+    table = CosSinTable(ROPE_BASE, 14, 64, device=DEV)
+    B, H, N, D = q.shape
+    rope = table.packed()
+    scale = 1 / math.sqrt(D)
+    o, lse = torch.ops.farope.attn_fwd(q, k, v, rope, N - 1, True, scale, _lib.BF16)
+    dq, dk, dv = torch.ops.farope.attn_bwd(do, q, k, v, o, lse, rope, N - 1, True, scale, _lib.BF16)
+    desc = _lib.make_desc(B, H, N, D, N - 1, True, _lib.BF16, _lib.BF16, scale)
+    delta = torch.empty(B, H, N, device=DEV, dtype=torch.float32)
+    dq2, dk2, dv2 = (torch.empty_like(q) for _ in range(3))
+    _lib.attn_bwd_preprocess(desc, o, do, delta)
+    _lib.attn_bwd_dk_dv(desc, q, k, v, do, lse, delta, rope, dk2, dv2)
+    _lib.attn_bwd_dq(desc, q, k, v, do, lse, delta, rope, dq2)
+    torch.cuda.synchronize()
+    ref_delta = (do.float() * o.float()).sum(-1)
+    assert errors(delta, ref_delta)[0] < 1e-3
+    for name, a, b in (("dQ", dq2, dq), ("dK", dk2, dk), ("dV", dv2, dv)):
+        mx, _ = errors(a, b)
+        _say(f"[split-vs-fused] {name}: max diff {mx:.3e}")
+        assert mx < 1e-2
+
+
+def test_deterministic():
+    cfg = dict(CONFIGS["vit_b"], B=8)
+    q, k, v, do = make_inputs(cfg, DEV)
+    table = CosSinTable(ROPE_BASE, 14, 64, device=DEV)
+    a = _run_ours(q, k, v, do, table, True)
+    b = _run_ours(q, k, v, do, table, True)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def test_large_logits_finite():
+    """Inputs x4 (logits std ~16): softmax must stay finite and accurate."""
+    cfg = dict(CONFIGS["vit_b"], B=4, scale=4.0)
+    q, k, v, do = make_inputs(cfg, DEV)
+    table = CosSinTable(ROPE_BASE, 14, 64, device=DEV)
+    ours = _run_ours(q, k, v, do, table, True)
+    for t in ours:
+        assert torch.isfinite(t).all()
+    ref = _ref(q, k, v, do, table, True)
+    other = _torch_bf16(q, k, v, do, table, True)
+    # Logits with std ~16: bf16 operands cannot resolve near-ties, so the
+    # bound here is "no worse than torch-ROCm bf16 SDPA + RoPE" (+25%).
+    for i, name in enumerate(("O", "dQ", "dK", "dV")):
+        mx, mn = errors(ours[i], ref[i])
+        omx, omn = errors(other[i], ref[i])
+        _say(f"[x4 inputs] {name}: ours max {mx:.3e} mean {mn:.3e} | torch-bf16 max {omx:.3e} mean {omn:.3e}")
+        assert mn <= 1.25 * omn + 1e-4, name

@@ -1,0 +1,124 @@
+"""The C ABI library: loads, exports every symbol include/farope.h declares,
+and rejects bad arguments on the host before launching anything.
+
+No call here reaches a kernel launch (no GPU in the CPU tier): only the
+host-only functions and argument-error paths are exercised.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from triton_fused_rope_flash_attn_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "farope.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        from triton_fused_rope_flash_attn_amd import build
+
+        build.build()
+    return _lib.load()
+
+
+def _header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(farope_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert sorted(_lib.EXPORTS) == _header_functions()
+
+
+def test_library_exports_every_header_symbol(lib):
+    for name in _header_functions():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_matches_header(lib):
+    m = re.search(r"#define FAROPE_ABI_VERSION (\d+)", open(HEADER).read())
+    assert lib.farope_abi_version() == int(m.group(1))
+
+
+def test_desc_struct_layout():
+    assert ctypes.sizeof(_lib.AttnDesc) == 9 * 4
+
+
+def test_strerror_covers_all_codes(lib):
+    texts = {rc: _lib.strerror(rc) for rc in range(0, 9)}
+    assert texts[0] == "success"
+    assert len(set(texts.values())) == 9
+    assert "unknown" in _lib.strerror(1234)
+
+
+def test_rope_packed_elems(lib):
+    assert lib.farope_rope_packed_elems(196, 32) == 197 * 32 * 2
+    assert lib.farope_rope_packed_elems(1024, 64) == 1025 * 128
+
+
+@pytest.mark.parametrize(
+    "N,D,has_cls,fwd_var,bwd_var",
+    [(197, 64, 1, 0, 0), (256, 64, 0, 0, 0), (257, 64, 1, 1, 1), (1025, 128, 1, 1, 1), (197, 128, 1, 1, 1)],
+)
+def test_tile_table(lib, N, D, has_cls, fwd_var, bwd_var):
+    desc = _lib.make_desc(8, 12, N, D, N - has_cls, has_cls, _lib.BF16, _lib.BF16, D ** -0.5)
+    f = _lib.tile_config(desc, 0)
+    b = _lib.tile_config(desc, 1)
+    assert f[0] == fwd_var and b[0] == bwd_var
+    assert f[1] * f[2] >= N and b[1] * b[2] >= N      # blocks cover the sequence
+    assert (f[2] - 1) * f[1] < N and (b[2] - 1) * b[1] < N  # and no empty block
+    assert f[3] % 64 == 0 and b[3] % 64 == 0
+
+
+def _call_fwd(lib, desc, q=16, lse=16, rope=16):
+    s = _lib.Stride4(0, 0, 0, 1)
+    return lib.farope_attn_fwd(
+        ctypes.byref(desc) if desc is not None else None,
+        q, s, 16, s, 16, s, rope, 16, s, lse, None,
+    )
+
+
+@pytest.mark.parametrize(
+    "kwargs,expect",
+    [
+        (dict(D=66), _lib.ERR_HEAD_DIM),
+        (dict(D=96), _lib.ERR_HEAD_DIM),
+        (dict(N=198), _lib.ERR_SEQ_LEN),
+        (dict(io=7), _lib.ERR_DTYPE),
+        (dict(ct=9), _lib.ERR_DTYPE),
+        (dict(B=0), _lib.ERR_SHAPE),
+    ],
+)
+def test_fwd_rejects_bad_descriptors(lib, kwargs, expect):
+    a = dict(B=2, H=3, N=197, D=64, io=_lib.BF16, ct=_lib.BF16)
+    a.update(kwargs)
+    desc = _lib.make_desc(a["B"], a["H"], a["N"], a["D"], 196, True, a["io"], a["ct"], 0.125)
+    assert _call_fwd(lib, desc) == expect
+
+
+def test_fwd_rejects_null_and_misaligned(lib):
+    assert _call_fwd(lib, None) == _lib.ERR_NULL
+    desc = _lib.make_desc(2, 3, 197, 64, 196, True, _lib.BF16, _lib.BF16, 0.125)
+    assert _call_fwd(lib, desc, q=None) == _lib.ERR_NULL
+    assert _call_fwd(lib, desc, q=17) == _lib.ERR_ALIGN       # bf16 needs 2-byte alignment
+    assert _call_fwd(lib, desc, rope=24) == _lib.ERR_ALIGN    # table needs 16-byte alignment
+
+
+def test_bwd_entry_points_reject_bad_arguments(lib):
+    s = _lib.Stride4(0, 0, 0, 1)
+    bad = _lib.make_desc(2, 3, 197, 60, 196, True, _lib.BF16, _lib.BF16, 0.125)
+    assert lib.farope_attn_bwd(ctypes.byref(bad), *([16, s] * 5), 16, 16, *([16, s] * 3), 16, None) == _lib.ERR_HEAD_DIM
+    good = _lib.make_desc(2, 3, 197, 64, 196, True, _lib.BF16, _lib.BF16, 0.125)
+    assert lib.farope_attn_bwd(ctypes.byref(good), *([16, s] * 5), None, 16, *([16, s] * 3), 16, None) == _lib.ERR_NULL
+    assert lib.farope_attn_bwd_preprocess(ctypes.byref(bad), 16, s, 16, s, 16, None) == _lib.ERR_HEAD_DIM
+    assert lib.farope_attn_bwd_dq(ctypes.byref(good), *([16, s] * 4), 16, 3, 16, 16, s, None) == _lib.ERR_ALIGN
+    assert lib.farope_attn_bwd_dk_dv(ctypes.byref(good), *([16, s] * 4), 16, 16, 16, 16, s, None, s, None) == _lib.ERR_NULL
+    assert lib.farope_rope_pack(16, 32, 1, 16, 32, 1, 196, 31, 16, None) == _lib.ERR_TABLE
+    assert lib.farope_rope_pack(None, 32, 1, 16, 32, 1, 196, 32, 16, None) == _lib.ERR_NULL

@@ -1,0 +1,302 @@
+// C-ABI layer: argument validation, the tile table, and kernel dispatch.
+// Declarations and per-function reference citations: include/farope.h.
+#include "farope.h"
+
+#include <hip/hip_runtime.h>
+
+#include "params.h"
+
+using namespace farope;
+
+namespace {
+
+constexpr int kPlaneMaxN = 256;   // fused / plane-resident kernels hold <= 256 rows of a plane
+
+int elem_size(int dt) { return dt == FAROPE_F32 ? 4 : 2; }
+
+bool dtype_ok(int dt) { return dt == FAROPE_F32 || dt == FAROPE_F16 || dt == FAROPE_BF16; }
+
+int check_desc(const farope_attn_desc* d) {
+  if (!d) return FAROPE_ERR_NULL;
+  if (d->batch <= 0 || d->heads <= 0) return FAROPE_ERR_SHAPE;
+  if ((int64_t)d->batch * d->heads > (int64_t)(1 << 30)) return FAROPE_ERR_SHAPE;
+  if (d->head_dim <= 0 || d->head_dim % 4 != 0) return FAROPE_ERR_HEAD_DIM;
+  if (d->head_dim != 64 && d->head_dim != 128) return FAROPE_ERR_HEAD_DIM;
+  if (d->has_cls != 0 && d->has_cls != 1) return FAROPE_ERR_SEQ_LEN;
+  if (d->n_pos < 1 || d->seq_len != d->n_pos + d->has_cls) return FAROPE_ERR_SEQ_LEN;
+  if (!dtype_ok(d->io_dtype) || !dtype_ok(d->compute_dtype)) return FAROPE_ERR_DTYPE;
+  return FAROPE_OK;
+}
+
+int check_ptr(const void* p, int es) {
+  if (!p) return FAROPE_ERR_NULL;
+  if (reinterpret_cast<uintptr_t>(p) % es) return FAROPE_ERR_ALIGN;
+  return FAROPE_OK;
+}
+
+// 16-byte vector path allowed: unit channel stride and 16-byte aligned rows.
+int vec_ok(const void* p, const int64_t s[4], int es) {
+  if (s[3] != 1) return 0;
+  if (reinterpret_cast<uintptr_t>(p) % 16) return 0;
+  for (int i = 0; i < 3; ++i)
+    if ((s[i] * es) % 16 != 0) return 0;
+  return 1;
+}
+
+void copy4(int64_t dst[4], const int64_t src[4]) {
+  for (int i = 0; i < 4; ++i) dst[i] = src[i];
+}
+
+bool fwd_plane(const farope_attn_desc* d) { return d->head_dim == 64 && d->seq_len <= kPlaneMaxN; }
+bool bwd_fused(const farope_attn_desc* d) { return d->head_dim == 64 && d->seq_len <= kPlaneMaxN; }
+
+int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+int fill_common(BwdParams& p, const farope_attn_desc* d, const float* rope) {
+  p.rope = rope;
+  p.B = d->batch;
+  p.H = d->heads;
+  p.N = d->seq_len;
+  p.has_cls = d->has_cls;
+  p.scale = d->softmax_scale;
+  p.scale_log2 = d->softmax_scale * 1.4426950408889634f;
+  return FAROPE_OK;
+}
+
+#define FAROPE_TRY(expr)            \
+  do {                              \
+    const int rc__ = (expr);        \
+    if (rc__ != FAROPE_OK) return rc__; \
+  } while (0)
+
+int launch_rc(hipError_t e) { return e == hipSuccess ? FAROPE_OK : FAROPE_ERR_LAUNCH; }
+
+}  // namespace
+
+extern "C" {
+
+int farope_abi_version(void) { return FAROPE_ABI_VERSION; }
+
+const char* farope_strerror(int status) {
+  switch (status) {
+    case FAROPE_OK: return "success";
+    case FAROPE_ERR_NULL: return "farope: a required pointer is NULL";
+    case FAROPE_ERR_HEAD_DIM:
+      return "farope: unsupported head_dim (must be divisible by 4; kernels exist for 64 and 128)";
+    case FAROPE_ERR_SEQ_LEN: return "farope: seq_len must equal n_pos + has_cls";
+    case FAROPE_ERR_DTYPE: return "farope: unsupported dtype (float32, float16, bfloat16)";
+    case FAROPE_ERR_TABLE: return "farope: RoPE table geometry does not match the call";
+    case FAROPE_ERR_SHAPE: return "farope: batch/heads must be positive and B*H <= 2^30";
+    case FAROPE_ERR_LAUNCH: return "farope: HIP kernel launch failed";
+    case FAROPE_ERR_ALIGN: return "farope: pointer not aligned to its element size";
+    default: return "farope: unknown status";
+  }
+}
+
+size_t farope_rope_packed_elems(int32_t n_pos, int32_t d2) {
+  if (n_pos < 0 || d2 < 0) return 0;
+  return (size_t)(n_pos + 1) * (size_t)d2 * 2;
+}
+
+int farope_rope_pack(const float* cosp, int64_t cos_stride0, int64_t cos_stride1,
+                     const float* sinp, int64_t sin_stride0, int64_t sin_stride1,
+                     int32_t n_pos, int32_t d2, float* packed, void* stream) {
+  if (!cosp || !sinp || !packed) return FAROPE_ERR_NULL;
+  if (n_pos < 1 || d2 < 1 || d2 % 2 != 0) return FAROPE_ERR_TABLE;
+  if (reinterpret_cast<uintptr_t>(packed) % 16) return FAROPE_ERR_ALIGN;
+  return launch_rc(launch_rope_pack(cosp, cos_stride0, cos_stride1, sinp, sin_stride0,
+                                    sin_stride1, n_pos, d2, packed,
+                                    static_cast<hipStream_t>(stream)));
+}
+
+int farope_tile_config(const farope_attn_desc* desc, int32_t which, int32_t out[4]) {
+  FAROPE_TRY(check_desc(desc));
+  if (!out) return FAROPE_ERR_NULL;
+  const int D = desc->head_dim, N = desc->seq_len;
+  if (which == 0) {
+    const int var = fwd_plane(desc) ? FWD_PLANE : FWD_STREAM;
+    const int rows = fwd_block_rows(D, var);
+    out[0] = var;
+    out[1] = rows;
+    out[2] = cdiv(N, rows);
+    out[3] = var == FWD_PLANE ? 512 : 256;
+  } else {
+    const bool fu = bwd_fused(desc);
+    out[0] = fu ? BWD_FUSED : BWD_SPLIT;
+    out[1] = fu ? bwd_dkdv_block_rows(D, true) : bwd_dkdv_block_rows(D, false);
+    out[2] = cdiv(N, out[1]);
+    out[3] = fu ? 512 : 256;
+  }
+  return FAROPE_OK;
+}
+
+int farope_attn_fwd(const farope_attn_desc* desc, const void* q, const int64_t q_stride[4],
+                    const void* k, const int64_t k_stride[4], const void* v,
+                    const int64_t v_stride[4], const float* rope_packed, void* o,
+                    const int64_t o_stride[4], float* lse, void* stream) {
+  FAROPE_TRY(check_desc(desc));
+  if (!q_stride || !k_stride || !v_stride || !o_stride) return FAROPE_ERR_NULL;
+  const int es = elem_size(desc->io_dtype);
+  FAROPE_TRY(check_ptr(q, es));
+  FAROPE_TRY(check_ptr(k, es));
+  FAROPE_TRY(check_ptr(v, es));
+  FAROPE_TRY(check_ptr(o, es));
+  FAROPE_TRY(check_ptr(lse, 4));
+  FAROPE_TRY(check_ptr(rope_packed, 16));
+
+  FwdParams p;
+  p.q = q; p.k = k; p.v = v; p.o = o; p.lse = lse;
+  copy4(p.sq, q_stride); copy4(p.sk, k_stride); copy4(p.sv, v_stride); copy4(p.so, o_stride);
+  p.rope = rope_packed;
+  p.B = desc->batch; p.H = desc->heads; p.N = desc->seq_len; p.has_cls = desc->has_cls;
+  p.scale_log2 = desc->softmax_scale * 1.4426950408889634f;
+  p.vec_q = vec_ok(q, q_stride, es);
+  p.vec_k = vec_ok(k, k_stride, es);
+  p.vec_v = vec_ok(v, v_stride, es);
+  p.vec_o = vec_ok(o, o_stride, es);
+  const int var = fwd_plane(desc) ? FWD_PLANE : FWD_STREAM;
+  p.n_blk = cdiv(p.N, fwd_block_rows(desc->head_dim, var));
+  return launch_rc(launch_fwd(p, desc->io_dtype, desc->compute_dtype, desc->head_dim, var,
+                              static_cast<hipStream_t>(stream)));
+}
+
+int farope_attn_bwd_preprocess(const farope_attn_desc* desc, const void* o,
+                               const int64_t o_stride[4], const void* dout,
+                               const int64_t dout_stride[4], float* delta, void* stream) {
+  FAROPE_TRY(check_desc(desc));
+  if (!o_stride || !dout_stride) return FAROPE_ERR_NULL;
+  const int es = elem_size(desc->io_dtype);
+  FAROPE_TRY(check_ptr(o, es));
+  FAROPE_TRY(check_ptr(dout, es));
+  FAROPE_TRY(check_ptr(delta, 4));
+  BwdParams p = {};
+  fill_common(p, desc, nullptr);
+  p.o = o; p.dout = dout; p.delta = delta;
+  copy4(p.so, o_stride); copy4(p.sdo, dout_stride);
+  p.vec_o = vec_ok(o, o_stride, es);
+  p.vec_do = vec_ok(dout, dout_stride, es);
+  return launch_rc(launch_bwd_pre(p, desc->io_dtype, desc->head_dim,
+                                  static_cast<hipStream_t>(stream)));
+}
+
+int farope_attn_bwd_dk_dv(const farope_attn_desc* desc, const void* q, const int64_t q_stride[4],
+                          const void* k, const int64_t k_stride[4], const void* v,
+                          const int64_t v_stride[4], const void* dout,
+                          const int64_t dout_stride[4], const float* lse, const float* delta,
+                          const float* rope_packed, void* dk, const int64_t dk_stride[4],
+                          void* dv, const int64_t dv_stride[4], void* stream) {
+  FAROPE_TRY(check_desc(desc));
+  if (!q_stride || !k_stride || !v_stride || !dout_stride || !dk_stride || !dv_stride)
+    return FAROPE_ERR_NULL;
+  const int es = elem_size(desc->io_dtype);
+  FAROPE_TRY(check_ptr(q, es));
+  FAROPE_TRY(check_ptr(k, es));
+  FAROPE_TRY(check_ptr(v, es));
+  FAROPE_TRY(check_ptr(dout, es));
+  FAROPE_TRY(check_ptr(dk, es));
+  FAROPE_TRY(check_ptr(dv, es));
+  FAROPE_TRY(check_ptr(lse, 4));
+  FAROPE_TRY(check_ptr(delta, 4));
+  FAROPE_TRY(check_ptr(rope_packed, 16));
+  BwdParams p = {};
+  fill_common(p, desc, rope_packed);
+  p.q = q; p.k = k; p.v = v; p.dout = dout; p.dk = dk; p.dv = dv;
+  p.lse = lse; p.delta = const_cast<float*>(delta);
+  copy4(p.sq, q_stride); copy4(p.sk, k_stride); copy4(p.sv, v_stride);
+  copy4(p.sdo, dout_stride); copy4(p.sdk, dk_stride); copy4(p.sdv, dv_stride);
+  p.vec_q = vec_ok(q, q_stride, es);
+  p.vec_k = vec_ok(k, k_stride, es);
+  p.vec_v = vec_ok(v, v_stride, es);
+  p.vec_do = vec_ok(dout, dout_stride, es);
+  p.vec_dk = vec_ok(dk, dk_stride, es);
+  p.vec_dv = vec_ok(dv, dv_stride, es);
+  p.n_blk = cdiv(p.N, bwd_dkdv_block_rows(desc->head_dim, false));
+  return launch_rc(launch_bwd_dkdv(p, desc->io_dtype, desc->compute_dtype, desc->head_dim, false,
+                                   static_cast<hipStream_t>(stream)));
+}
+
+int farope_attn_bwd_dq(const farope_attn_desc* desc, const void* q, const int64_t q_stride[4],
+                       const void* k, const int64_t k_stride[4], const void* v,
+                       const int64_t v_stride[4], const void* dout, const int64_t dout_stride[4],
+                       const float* lse, const float* delta, const float* rope_packed, void* dq,
+                       const int64_t dq_stride[4], void* stream) {
+  FAROPE_TRY(check_desc(desc));
+  if (!q_stride || !k_stride || !v_stride || !dout_stride || !dq_stride) return FAROPE_ERR_NULL;
+  const int es = elem_size(desc->io_dtype);
+  FAROPE_TRY(check_ptr(q, es));
+  FAROPE_TRY(check_ptr(k, es));
+  FAROPE_TRY(check_ptr(v, es));
+  FAROPE_TRY(check_ptr(dout, es));
+  FAROPE_TRY(check_ptr(dq, es));
+  FAROPE_TRY(check_ptr(lse, 4));
+  FAROPE_TRY(check_ptr(delta, 4));
+  FAROPE_TRY(check_ptr(rope_packed, 16));
+  BwdParams p = {};
+  fill_common(p, desc, rope_packed);
+  p.q = q; p.k = k; p.v = v; p.dout = dout; p.dq = dq;
+  p.lse = lse; p.delta = const_cast<float*>(delta);
+  copy4(p.sq, q_stride); copy4(p.sk, k_stride); copy4(p.sv, v_stride);
+  copy4(p.sdo, dout_stride); copy4(p.sdq, dq_stride);
+  p.vec_q = vec_ok(q, q_stride, es);
+  p.vec_k = vec_ok(k, k_stride, es);
+  p.vec_v = vec_ok(v, v_stride, es);
+  p.vec_do = vec_ok(dout, dout_stride, es);
+  p.vec_dq = vec_ok(dq, dq_stride, es);
+  p.n_blk = cdiv(p.N, bwd_dq_block_rows(desc->head_dim));
+  return launch_rc(launch_bwd_dq(p, desc->io_dtype, desc->compute_dtype, desc->head_dim, false,
+                                 static_cast<hipStream_t>(stream)));
+}
+
+int farope_attn_bwd(const farope_attn_desc* desc, const void* q, const int64_t q_stride[4],
+                    const void* k, const int64_t k_stride[4], const void* v,
+                    const int64_t v_stride[4], const void* o, const int64_t o_stride[4],
+                    const void* dout, const int64_t dout_stride[4], const float* lse,
+                    const float* rope_packed, void* dq, const int64_t dq_stride[4], void* dk,
+                    const int64_t dk_stride[4], void* dv, const int64_t dv_stride[4],
+                    float* delta_ws, void* stream) {
+  FAROPE_TRY(check_desc(desc));
+  if (!q_stride || !k_stride || !v_stride || !o_stride || !dout_stride || !dq_stride ||
+      !dk_stride || !dv_stride)
+    return FAROPE_ERR_NULL;
+  const int es = elem_size(desc->io_dtype);
+  FAROPE_TRY(check_ptr(q, es));
+  FAROPE_TRY(check_ptr(k, es));
+  FAROPE_TRY(check_ptr(v, es));
+  FAROPE_TRY(check_ptr(o, es));
+  FAROPE_TRY(check_ptr(dout, es));
+  FAROPE_TRY(check_ptr(dq, es));
+  FAROPE_TRY(check_ptr(dk, es));
+  FAROPE_TRY(check_ptr(dv, es));
+  FAROPE_TRY(check_ptr(lse, 4));
+  FAROPE_TRY(check_ptr(rope_packed, 16));
+  const bool fused = bwd_fused(desc);
+  if (!fused) FAROPE_TRY(check_ptr(delta_ws, 4));
+  BwdParams p = {};
+  fill_common(p, desc, rope_packed);
+  p.q = q; p.k = k; p.v = v; p.o = o; p.dout = dout;
+  p.dq = dq; p.dk = dk; p.dv = dv;
+  p.lse = lse; p.delta = delta_ws;
+  copy4(p.sq, q_stride); copy4(p.sk, k_stride); copy4(p.sv, v_stride); copy4(p.so, o_stride);
+  copy4(p.sdo, dout_stride); copy4(p.sdq, dq_stride); copy4(p.sdk, dk_stride);
+  copy4(p.sdv, dv_stride);
+  p.vec_q = vec_ok(q, q_stride, es);
+  p.vec_k = vec_ok(k, k_stride, es);
+  p.vec_v = vec_ok(v, v_stride, es);
+  p.vec_o = vec_ok(o, o_stride, es);
+  p.vec_do = vec_ok(dout, dout_stride, es);
+  p.vec_dq = vec_ok(dq, dq_stride, es);
+  p.vec_dk = vec_ok(dk, dk_stride, es);
+  p.vec_dv = vec_ok(dv, dv_stride, es);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const int D = desc->head_dim;
+  if (fused) {
+    p.n_blk = 1;
+    return launch_rc(launch_bwd_dkdv(p, desc->io_dtype, desc->compute_dtype, D, true, st));
+  }
+  p.n_blk = cdiv(p.N, bwd_dq_block_rows(D));
+  FAROPE_TRY(launch_rc(launch_bwd_dq(p, desc->io_dtype, desc->compute_dtype, D, true, st)));
+  p.n_blk = cdiv(p.N, bwd_dkdv_block_rows(D, false));
+  return launch_rc(launch_bwd_dkdv(p, desc->io_dtype, desc->compute_dtype, D, false, st));
+}
+
+}  // extern "C"

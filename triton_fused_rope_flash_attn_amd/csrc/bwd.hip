@@ -1,0 +1,643 @@
+// Backward kernels for the fused 2D-RoPE attention.
+//
+// Reference behaviour followed ("fa_rope_full .py"):
+//   delta = rowsum(dO * O) in fp32                      _attn_bwd_preprocess FA:325-357
+//   P = exp(S - LSE), dV += P^T dO, dS = P*(dP - delta),
+//   dK-hat += dS^T Q-hat, dK = R^T dK-hat * scale       _attn_bwd_dk_dv_rope FA:374-691
+//   dQ-hat += dS K-hat,  dQ = R^T dQ-hat * scale        _attn_bwd_dq_rope    FA:708-1009
+// with the CLS row bypassing the rotation (FA:647-662, FA:980-993).
+//
+// gfx950 design (fragment conventions in common.h):
+//  * dK/dV kernel (KV-outer): each wave keeps its K-hat and V rows in
+//    registers as B-operands.  Per 32-query block it computes S and dP
+//    (query rows permuted so that lane group lg holds queries 8lg..8lg+7),
+//    so P and dS land directly in the B-operand layout of
+//    dV^T += dO^T P and dK-hat^T += Q-hat^T dS; dO^T and Q-hat^T are staged
+//    transposed in LDS once per query stage and shared by all waves.
+//  * Fused variant (N <= 256): one workgroup owns a whole (b, h) plane, so
+//    all keys of a query stage are on-chip.  dS of the stage is written to
+//    LDS and the same workgroup finishes dQ-hat^T = K-hat^T dS^T for that
+//    stage before moving on: S, P and dP are computed once, delta is formed
+//    while staging O and dO, and Q, K, V, O, dO are each read from HBM once.
+//  * dQ kernel (Q-outer, any N): logits transposed as in the forward pass;
+//    dS^T lands in the B-operand layout of dQ-hat^T += K-hat^T dS^T.  It
+//    can produce delta itself, so the split path needs no separate
+//    preprocessing launch.
+#include "common.h"
+#include "params.h"
+
+namespace farope {
+
+// ---------------------------------------------------------------------------
+// delta = rowsum(dO * O)  (fp32), one row per D/8 consecutive threads.
+// ---------------------------------------------------------------------------
+template <typename IO, int D>
+__global__ void __launch_bounds__(256) bwd_pre_kernel(const BwdParams p) {
+  constexpr int CPR = D / 8;
+  constexpr int RPB = 256 / CPR;
+  const int64_t grow = (int64_t)blockIdx.x * RPB + threadIdx.x / CPR;
+  const int cc = threadIdx.x % CPR;
+  const int64_t total = (int64_t)p.B * p.H * p.N;
+  float acc = 0.f;
+  if (grow < total) {
+    const int plane = (int)(grow / p.N);
+    const int row = (int)(grow - (int64_t)plane * p.N);
+    const int bb = plane / p.H, hh = plane - bb * p.H;
+    const IO* O = static_cast<const IO*>(p.o) + bb * p.so[0] + hh * p.so[1] + row * p.so[2];
+    const IO* G = static_cast<const IO*>(p.dout) + bb * p.sdo[0] + hh * p.sdo[1] + row * p.sdo[2];
+    float o[8], g[8];
+    load8(O + 8 * cc * p.so[3], p.so[3], p.vec_o, o);
+    load8(G + 8 * cc * p.sdo[3], p.sdo[3], p.vec_do, g);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc += o[e] * g[e];
+  }
+#pragma unroll
+  for (int m = 1; m < CPR; m <<= 1) acc += __shfl_xor(acc, m);
+  if (grow < total && cc == 0) p.delta[grow] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// dQ kernel (Q-outer).
+// ---------------------------------------------------------------------------
+template <typename IO, int CT, int D, int NW, int QT, int KVS, bool WRITE_DELTA>
+__global__ void __launch_bounds__(NW * 64)
+bwd_dq_kernel(const BwdParams p) {
+  using C = Comp<CT>;
+  using S = typename C::S;
+  using Frag = typename C::Frag;
+  constexpr int KS = D / 32, DT = D / 16, D2 = D / 2;
+  constexpr int PADE = 16 / sizeof(S);
+  constexpr int LDK = D + PADE, LDT = KVS + PADE;
+  constexpr int NT = NW * 64, CPR = D / 8;
+  constexpr int ITER = (KVS * CPR + NT - 1) / NT;
+  constexpr int QROWS = NW * QT * 16;
+
+  __shared__ __attribute__((aligned(16))) S sK[KVS * LDK];
+  __shared__ __attribute__((aligned(16))) S sKt[D * LDT];
+  __shared__ __attribute__((aligned(16))) S sV[KVS * LDK];
+
+  const int N = p.N;
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int plane = tile / p.n_blk;
+  const int qblk = tile - plane * p.n_blk;
+  const int bb = plane / p.H, hh = plane - bb * p.H;
+  const IO* __restrict__ Q = static_cast<const IO*>(p.q) + bb * p.sq[0] + hh * p.sq[1];
+  const IO* __restrict__ K = static_cast<const IO*>(p.k) + bb * p.sk[0] + hh * p.sk[1];
+  const IO* __restrict__ V = static_cast<const IO*>(p.v) + bb * p.sv[0] + hh * p.sv[1];
+  const IO* __restrict__ O = static_cast<const IO*>(p.o) + bb * p.so[0] + hh * p.so[1];
+  const IO* __restrict__ G = static_cast<const IO*>(p.dout) + bb * p.sdo[0] + hh * p.sdo[1];
+  IO* __restrict__ dQ = static_cast<IO*>(p.dq) + bb * p.sdq[0] + hh * p.sdq[1];
+  const float* __restrict__ tab = p.rope;
+  const int shift = 1 - p.has_cls;
+  const int64_t prow = (int64_t)plane * N;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int lr = lane & 15, lg = lane >> 4;
+
+  Frag qf[QT][KS], gf[QT][KS];
+  float lse2[QT], dlt[QT];
+  int qrow[QT];
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    const int row = qblk * QROWS + (wave * QT + t) * 16 + lr;
+    qrow[t] = row;
+    float dsum = 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int c0 = 32 * s + 8 * lg;
+      float x[8], g[8];
+      if (row < N) {
+        load8(Q + row * p.sq[2] + c0 * p.sq[3], p.sq[3], p.vec_q, x);
+        float cs[8];
+        rope_load4(tab, row + shift, D2, c0 / 2, cs);
+        rope_rotate8(x, cs);
+        load8(G + row * p.sdo[2] + c0 * p.sdo[3], p.sdo[3], p.vec_do, g);
+        if (WRITE_DELTA) {
+          float o[8];
+          load8(O + row * p.so[2] + c0 * p.so[3], p.so[3], p.vec_o, o);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dsum += g[e] * o[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = g[e] = 0.f;
+      }
+      qf[t][s] = C::make(x);
+      gf[t][s] = C::make(g);
+    }
+    if (WRITE_DELTA) {
+      dsum = group4_sum(dsum);
+      if (lg == 0 && row < N) p.delta[prow + row] = dsum;
+      dlt[t] = dsum;
+    } else {
+      dlt[t] = row < N ? p.delta[prow + row] : 0.f;
+    }
+    lse2[t] = row < N ? p.lse[prow + row] * kLog2e : 0.f;
+  }
+  const bool wave_active = qblk * QROWS + wave * QT * 16 < N;
+
+  f32x4 dqacc[QT][DT];
+#pragma unroll
+  for (int t = 0; t < QT; ++t)
+#pragma unroll
+    for (int d = 0; d < DT; ++d) dqacc[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int kvb = 0; kvb < N; kvb += KVS) {
+    const int rows = min(KVS, round_up32(N - kvb));
+    if (kvb > 0) __syncthreads();
+    {
+      float xk[ITER][8], xv[ITER][8], cs[ITER][8];
+#pragma unroll
+      for (int it = 0; it < ITER; ++it) {
+        const int c = tid + it * NT;
+        const int r = c / CPR, cc = c - r * CPR, gr = kvb + r;
+        if (c < rows * CPR && gr < N) {
+          load8(K + gr * p.sk[2] + 8 * cc * p.sk[3], p.sk[3], p.vec_k, xk[it]);
+          load8(V + gr * p.sv[2] + 8 * cc * p.sv[3], p.sv[3], p.vec_v, xv[it]);
+          rope_load4(tab, gr + shift, D2, 4 * cc, cs[it]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) { xk[it][e] = 0.f; xv[it][e] = 0.f; cs[it][e] = 0.f; }
+        }
+      }
+#pragma unroll
+      for (int it = 0; it < ITER; ++it) {
+        const int c = tid + it * NT;
+        const int r = c / CPR, cc = c - r * CPR;
+        if (c < rows * CPR) {
+          rope_rotate8(xk[it], cs[it]);
+          C::put8(&sK[r * LDK + 8 * cc], xk[it]);
+          C::put8(&sV[r * LDK + 8 * cc], xv[it]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) C::put1(&sKt[(8 * cc + e) * LDT + r], xk[it][e]);
+        }
+      }
+    }
+    __syncthreads();
+    if (!wave_active) continue;
+
+    for (int j = 0; j < rows / 32; ++j) {
+      f32x4 sacc[QT][2], pacc[QT][2];
+#pragma unroll
+      for (int t = 0; t < QT; ++t)
+        sacc[t][0] = sacc[t][1] = pacc[t][0] = pacc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int kl = 32 * j + 8 * (lr >> 2) + 4 * h + (lr & 3);
+          const Frag a = C::lds(&sK[kl * LDK + 32 * s + 8 * lg]);
+          const Frag b = C::lds(&sV[kl * LDK + 32 * s + 8 * lg]);
+#pragma unroll
+          for (int t = 0; t < QT; ++t) {
+            sacc[t][h] = C::mma(a, qf[t][s], sacc[t][h]);
+            pacc[t][h] = C::mma(b, gf[t][s], pacc[t][h]);
+          }
+        }
+      }
+      const int kbase = kvb + 32 * j + 8 * lg;
+      const bool full = kvb + 32 * j + 32 <= N;
+      Frag dsf[QT];
+#pragma unroll
+      for (int t = 0; t < QT; ++t) {
+        float ds[8];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const bool valid = full || kbase + 4 * h + i < N;
+            const float pr = valid ? fast_exp2(sacc[t][h][i] * p.scale_log2 - lse2[t]) : 0.f;
+            ds[4 * h + i] = pr * (pacc[t][h][i] - dlt[t]);
+          }
+        dsf[t] = C::make(ds);
+      }
+#pragma unroll
+      for (int d = 0; d < DT; ++d) {
+        const Frag a = C::lds(&sKt[(16 * d + lr) * LDT + 32 * j + 8 * lg]);
+#pragma unroll
+        for (int t = 0; t < QT; ++t) dqacc[t][d] = C::mma(a, dsf[t], dqacc[t][d]);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    const int row = qrow[t];
+    if (row < N) {
+#pragma unroll
+      for (int d = 0; d < DT; ++d) {
+        float g4[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) g4[r] = dqacc[t][d][r] * p.scale;
+        rope_unrotate4(g4, tab, row + shift, D2, 8 * d + 2 * lg);
+        store4(dQ + row * p.sdq[2] + (16 * d + 4 * lg) * p.sdq[3], p.sdq[3], p.vec_dq, g4);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dK/dV kernel (KV-outer); FUSED additionally produces dQ (whole plane per
+// workgroup, NKV >= N).
+// ---------------------------------------------------------------------------
+template <typename IO, int CT, int D, int NW, int KT, int QS, bool FUSED>
+__global__ void __launch_bounds__(NW * 64)
+bwd_dkdv_kernel(const BwdParams p) {
+  using C = Comp<CT>;
+  using S = typename C::S;
+  using Frag = typename C::Frag;
+  constexpr int KS = D / 32, DT = D / 16, D2 = D / 2;
+  constexpr int PADE = 16 / sizeof(S);
+  constexpr int LDQ = D + PADE, LDT = QS + PADE;
+  constexpr int NT = NW * 64, CPR = D / 8;
+  constexpr int ITER = (QS * CPR + NT - 1) / NT;
+  constexpr int KROWS = NW * KT * 16;           // kv rows per workgroup
+  constexpr int LDKT = KROWS + PADE;            // fused: K-hat^T / dS row pitch
+  constexpr int KITER = (KROWS * CPR + NT - 1) / NT;
+
+  __shared__ __attribute__((aligned(16))) S sQ[QS * LDQ];
+  __shared__ __attribute__((aligned(16))) S sQt[D * LDT];
+  __shared__ __attribute__((aligned(16))) S sG[QS * LDQ];
+  __shared__ __attribute__((aligned(16))) S sGt[D * LDT];
+  __shared__ __attribute__((aligned(16))) float sL2[QS];
+  __shared__ __attribute__((aligned(16))) float sDl[QS];
+  __shared__ __attribute__((aligned(16))) S sKt[FUSED ? D * LDKT : 8];
+  __shared__ __attribute__((aligned(16))) S sdS[FUSED ? QS * LDKT : 8];
+
+  const int N = p.N;
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int plane = tile / p.n_blk;
+  const int kblk = tile - plane * p.n_blk;
+  const int bb = plane / p.H, hh = plane - bb * p.H;
+  const IO* __restrict__ Q = static_cast<const IO*>(p.q) + bb * p.sq[0] + hh * p.sq[1];
+  const IO* __restrict__ K = static_cast<const IO*>(p.k) + bb * p.sk[0] + hh * p.sk[1];
+  const IO* __restrict__ V = static_cast<const IO*>(p.v) + bb * p.sv[0] + hh * p.sv[1];
+  const IO* __restrict__ O = static_cast<const IO*>(p.o) + bb * p.so[0] + hh * p.so[1];
+  const IO* __restrict__ G = static_cast<const IO*>(p.dout) + bb * p.sdo[0] + hh * p.sdo[1];
+  IO* __restrict__ dQ = static_cast<IO*>(p.dq) + bb * p.sdq[0] + hh * p.sdq[1];
+  IO* __restrict__ dK = static_cast<IO*>(p.dk) + bb * p.sdk[0] + hh * p.sdk[1];
+  IO* __restrict__ dV = static_cast<IO*>(p.dv) + bb * p.sdv[0] + hh * p.sdv[1];
+  const float* __restrict__ tab = p.rope;
+  const int shift = 1 - p.has_cls;
+  const int64_t prow = (int64_t)plane * N;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int kv_first = kblk * KROWS + wave * KT * 16;
+
+  // ---- this wave's K-hat and V rows as B-operands ----
+  Frag kf[KT][KS], vf[KT][KS];
+#pragma unroll
+  for (int u = 0; u < KT; ++u) {
+    const int row = kv_first + 16 * u + lr;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int c0 = 32 * s + 8 * lg;
+      float x[8], y[8];
+      if (row < N) {
+        load8(K + row * p.sk[2] + c0 * p.sk[3], p.sk[3], p.vec_k, x);
+        float cs[8];
+        rope_load4(tab, row + shift, D2, c0 / 2, cs);
+        rope_rotate8(x, cs);
+        load8(V + row * p.sv[2] + c0 * p.sv[3], p.sv[3], p.vec_v, y);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = y[e] = 0.f;
+      }
+      kf[u][s] = C::make(x);
+      vf[u][s] = C::make(y);
+    }
+  }
+
+  f32x4 dvacc[KT][DT], dkacc[KT][DT];
+#pragma unroll
+  for (int u = 0; u < KT; ++u)
+#pragma unroll
+    for (int d = 0; d < DT; ++d) dvacc[u][d] = dkacc[u][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int nkv32 = round_up32(N);   // fused: key columns held in sKt / sdS
+  if constexpr (FUSED) {
+    // K-hat^T of the whole plane (zero beyond N) and a zeroed dS buffer.
+    float xk[KITER][8], cs[KITER][8];
+#pragma unroll
+    for (int it = 0; it < KITER; ++it) {
+      const int c = tid + it * NT;
+      const int r = c / CPR, cc = c - r * CPR;
+      if (c < nkv32 * CPR && r < N) {
+        load8(K + r * p.sk[2] + 8 * cc * p.sk[3], p.sk[3], p.vec_k, xk[it]);
+        rope_load4(tab, r + shift, D2, 4 * cc, cs[it]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) { xk[it][e] = 0.f; cs[it][e] = 0.f; }
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < KITER; ++it) {
+      const int c = tid + it * NT;
+      const int r = c / CPR, cc = c - r * CPR;
+      if (c < nkv32 * CPR) {
+        rope_rotate8(xk[it], cs[it]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) C::put1(&sKt[(8 * cc + e) * LDKT + r], xk[it][e]);
+      }
+    }
+    for (int i = tid; i < QS * LDKT; i += NT) C::put1(&sdS[i], 0.f);
+  }
+
+  for (int qb = 0; qb < N; qb += QS) {
+    const int rows = min(QS, round_up32(N - qb));
+    __syncthreads();
+    // ---- stage Q-hat, Q-hat^T, dO, dO^T (+ delta, LSE) for this q stage ----
+    {
+      float xq[ITER][8], xg[ITER][8], cs[ITER][8], xo[ITER][8];
+#pragma unroll
+      for (int it = 0; it < ITER; ++it) {
+        const int c = tid + it * NT;
+        const int r = c / CPR, cc = c - r * CPR, gr = qb + r;
+        if (c < rows * CPR && gr < N) {
+          load8(Q + gr * p.sq[2] + 8 * cc * p.sq[3], p.sq[3], p.vec_q, xq[it]);
+          load8(G + gr * p.sdo[2] + 8 * cc * p.sdo[3], p.sdo[3], p.vec_do, xg[it]);
+          rope_load4(tab, gr + shift, D2, 4 * cc, cs[it]);
+          if (FUSED) load8(O + gr * p.so[2] + 8 * cc * p.so[3], p.so[3], p.vec_o, xo[it]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) { xq[it][e] = xg[it][e] = cs[it][e] = xo[it][e] = 0.f; }
+        }
+      }
+#pragma unroll
+      for (int it = 0; it < ITER; ++it) {
+        const int c = tid + it * NT;
+        const int r = c / CPR, cc = c - r * CPR;
+        if (FUSED) {
+          // delta for row r: the CPR chunks of a row sit in consecutive lanes.
+          float dsum = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dsum += xg[it][e] * xo[it][e];
+#pragma unroll
+          for (int m = 1; m < CPR; m <<= 1) dsum += __shfl_xor(dsum, m);
+          if (c < rows * CPR && cc == 0) sDl[r] = dsum;
+        }
+        if (c < rows * CPR) {
+          rope_rotate8(xq[it], cs[it]);
+          C::put8(&sQ[r * LDQ + 8 * cc], xq[it]);
+          C::put8(&sG[r * LDQ + 8 * cc], xg[it]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            C::put1(&sQt[(8 * cc + e) * LDT + r], xq[it][e]);
+            C::put1(&sGt[(8 * cc + e) * LDT + r], xg[it][e]);
+          }
+        }
+      }
+      for (int r = tid; r < rows; r += NT) {
+        const int gr = qb + r;
+        sL2[r] = gr < N ? p.lse[prow + gr] * kLog2e : INFINITY;
+        if (!FUSED) sDl[r] = gr < N ? p.delta[prow + gr] : 0.f;
+      }
+    }
+    __syncthreads();
+
+    for (int j = 0; j < rows / 32; ++j) {
+      float l2[8], dl[8];
+      {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(&sL2[32 * j + 8 * lg]);
+        const f32x4 b = *reinterpret_cast<const f32x4*>(&sL2[32 * j + 8 * lg + 4]);
+        const f32x4 c = *reinterpret_cast<const f32x4*>(&sDl[32 * j + 8 * lg]);
+        const f32x4 d = *reinterpret_cast<const f32x4*>(&sDl[32 * j + 8 * lg + 4]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { l2[e] = a[e]; l2[4 + e] = b[e]; dl[e] = c[e]; dl[4 + e] = d[e]; }
+      }
+#pragma unroll
+      for (int u = 0; u < KT; ++u) {
+        const int kv0 = kv_first + 16 * u;
+        if (kv0 >= N) continue;   // wave-uniform
+        f32x4 sacc[2], pacc[2];
+        sacc[0] = sacc[1] = pacc[0] = pacc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int ql = 32 * j + 8 * (lr >> 2) + 4 * h + (lr & 3);
+            const Frag a = C::lds(&sQ[ql * LDQ + 32 * s + 8 * lg]);
+            const Frag b = C::lds(&sG[ql * LDQ + 32 * s + 8 * lg]);
+            sacc[h] = C::mma(a, kf[u][s], sacc[h]);
+            pacc[h] = C::mma(b, vf[u][s], pacc[h]);
+          }
+        }
+        const bool kvalid = kv0 + lr < N;
+        float pv[8], dsv[8];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int e = 4 * h + i;
+            const float pr = kvalid ? fast_exp2(sacc[h][i] * p.scale_log2 - l2[e]) : 0.f;
+            pv[e] = pr;
+            dsv[e] = pr * (pacc[h][i] - dl[e]);
+          }
+        const Frag pf = C::make(pv);
+        const Frag dsf = C::make(dsv);
+#pragma unroll
+        for (int d = 0; d < DT; ++d) {
+          const Frag ag = C::lds(&sGt[(16 * d + lr) * LDT + 32 * j + 8 * lg]);
+          dvacc[u][d] = C::mma(ag, pf, dvacc[u][d]);
+          const Frag aq = C::lds(&sQt[(16 * d + lr) * LDT + 32 * j + 8 * lg]);
+          dkacc[u][d] = C::mma(aq, dsf, dkacc[u][d]);
+        }
+        if constexpr (FUSED) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) C::put1(&sdS[(32 * j + 8 * lg + e) * LDKT + kv0 + lr], dsv[e]);
+        }
+      }
+    }
+
+    if constexpr (FUSED) {
+      __syncthreads();
+      // dQ-hat^T[d, q] = sum_kv K-hat^T[d, kv] dS^T[kv, q] for this stage.
+      const int jobs = (rows / 16) * DT;
+      for (int job = wave; job < jobs; job += NW) {
+        const int qs = job / DT, d = job - qs * DT;
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int jj = 0; jj < nkv32 / 32; ++jj) {
+          const Frag a = C::lds(&sKt[(16 * d + lr) * LDKT + 32 * jj + 8 * lg]);
+          const Frag b = C::lds(&sdS[(16 * qs + lr) * LDKT + 32 * jj + 8 * lg]);
+          acc = C::mma(a, b, acc);
+        }
+        const int row = qb + 16 * qs + lr;
+        if (row < N) {
+          float g4[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) g4[r] = acc[r] * p.scale;
+          rope_unrotate4(g4, tab, row + shift, D2, 8 * d + 2 * lg);
+          store4(dQ + row * p.sdq[2] + (16 * d + 4 * lg) * p.sdq[3], p.sdq[3], p.vec_dq, g4);
+        }
+      }
+    }
+  }
+
+  // ---- epilogue: lane holds dV / dK-hat of kv row kv0 + lr, channels 16d + 4lg + (0..3) ----
+#pragma unroll
+  for (int u = 0; u < KT; ++u) {
+    const int row = kv_first + 16 * u + lr;
+    if (row < N) {
+#pragma unroll
+      for (int d = 0; d < DT; ++d) {
+        float v4[4], g4[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) { v4[r] = dvacc[u][d][r]; g4[r] = dkacc[u][d][r] * p.scale; }
+        store4(dV + row * p.sdv[2] + (16 * d + 4 * lg) * p.sdv[3], p.sdv[3], p.vec_dv, v4);
+        rope_unrotate4(g4, tab, row + shift, D2, 8 * d + 2 * lg);
+        store4(dK + row * p.sdk[2] + (16 * d + 4 * lg) * p.sdk[3], p.sdk[3], p.vec_dk, g4);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Tile table for the backward pass.
+// ---------------------------------------------------------------------------
+template <int D> struct BwdShape;
+template <> struct BwdShape<64> {
+  static constexpr int DQ_NW = 4, DQ_QT = 2, DQ_KVS = 64;
+  static constexpr int KV_NW = 4, KV_KT = 2, KV_QS = 64;
+  static constexpr int FU_NW = 8, FU_KT = 2, FU_QS = 32;   // 256 kv rows per workgroup
+};
+template <> struct BwdShape<128> {
+  static constexpr int DQ_NW = 4, DQ_QT = 1, DQ_KVS = 64;
+  static constexpr int KV_NW = 4, KV_KT = 1, KV_QS = 64;
+  static constexpr int FU_NW = 8, FU_KT = 1, FU_QS = 32;   // unused: D=128 uses the split path
+};
+
+int bwd_dq_block_rows(int D) {
+  return D == 64 ? BwdShape<64>::DQ_NW * BwdShape<64>::DQ_QT * 16
+                 : BwdShape<128>::DQ_NW * BwdShape<128>::DQ_QT * 16;
+}
+int bwd_dkdv_block_rows(int D, bool fused) {
+  if (D == 64)
+    return fused ? BwdShape<64>::FU_NW * BwdShape<64>::FU_KT * 16
+                 : BwdShape<64>::KV_NW * BwdShape<64>::KV_KT * 16;
+  return BwdShape<128>::KV_NW * BwdShape<128>::KV_KT * 16;
+}
+
+template <typename IO, int D>
+static hipError_t pre_io(const BwdParams& p, hipStream_t st) {
+  constexpr int RPB = 256 / (D / 8);
+  const int64_t total = (int64_t)p.B * p.H * p.N;
+  const int grid = (int)((total + RPB - 1) / RPB);
+  hipLaunchKernelGGL((bwd_pre_kernel<IO, D>), dim3(grid), dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_pre(const BwdParams& p, int io, int D, hipStream_t st) {
+  if (D == 64) {
+    switch (io) {
+      case DT_BF16: return pre_io<bf16, 64>(p, st);
+      case DT_F16: return pre_io<f16, 64>(p, st);
+      default: return pre_io<float, 64>(p, st);
+    }
+  }
+  switch (io) {
+    case DT_BF16: return pre_io<bf16, 128>(p, st);
+    case DT_F16: return pre_io<f16, 128>(p, st);
+    default: return pre_io<float, 128>(p, st);
+  }
+}
+
+template <typename IO, int CT, int D>
+static hipError_t dq_launch(const BwdParams& p, bool write_delta, hipStream_t st) {
+  using SH = BwdShape<D>;
+  const int grid = p.B * p.H * p.n_blk;
+  if (write_delta)
+    hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, true>),
+                       dim3(grid), dim3(SH::DQ_NW * 64), 0, st, p);
+  else
+    hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, false>),
+                       dim3(grid), dim3(SH::DQ_NW * 64), 0, st, p);
+  return hipGetLastError();
+}
+
+template <typename IO, int CT, int D>
+static hipError_t dkdv_launch(const BwdParams& p, bool fused, hipStream_t st) {
+  using SH = BwdShape<D>;
+  const int grid = p.B * p.H * p.n_blk;
+  if (fused && D == 64)
+    hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::FU_NW, SH::FU_KT, SH::FU_QS, true>),
+                       dim3(grid), dim3(SH::FU_NW * 64), 0, st, p);
+  else
+    hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS, false>),
+                       dim3(grid), dim3(SH::KV_NW * 64), 0, st, p);
+  return hipGetLastError();
+}
+
+template <typename IO, int D>
+static hipError_t dq_ct(const BwdParams& p, int ct, bool wd, hipStream_t st) {
+  switch (ct) {
+    case DT_BF16: return dq_launch<IO, DT_BF16, D>(p, wd, st);
+    case DT_F16: return dq_launch<IO, DT_F16, D>(p, wd, st);
+    default: return dq_launch<IO, DT_F32, D>(p, wd, st);
+  }
+}
+template <int D>
+static hipError_t dq_io(const BwdParams& p, int io, int ct, bool wd, hipStream_t st) {
+  switch (io) {
+    case DT_BF16: return dq_ct<bf16, D>(p, ct, wd, st);
+    case DT_F16: return dq_ct<f16, D>(p, ct, wd, st);
+    default: return dq_ct<float, D>(p, ct, wd, st);
+  }
+}
+hipError_t launch_bwd_dq(const BwdParams& p, int io, int ct, int D, bool write_delta,
+                         hipStream_t st) {
+  return D == 64 ? dq_io<64>(p, io, ct, write_delta, st) : dq_io<128>(p, io, ct, write_delta, st);
+}
+
+template <typename IO, int D>
+static hipError_t kv_ct(const BwdParams& p, int ct, bool fu, hipStream_t st) {
+  switch (ct) {
+    case DT_BF16: return dkdv_launch<IO, DT_BF16, D>(p, fu, st);
+    case DT_F16: return dkdv_launch<IO, DT_F16, D>(p, fu, st);
+    default: return dkdv_launch<IO, DT_F32, D>(p, fu, st);
+  }
+}
+template <int D>
+static hipError_t kv_io(const BwdParams& p, int io, int ct, bool fu, hipStream_t st) {
+  switch (io) {
+    case DT_BF16: return kv_ct<bf16, D>(p, ct, fu, st);
+    case DT_F16: return kv_ct<f16, D>(p, ct, fu, st);
+    default: return kv_ct<float, D>(p, ct, fu, st);
+  }
+}
+hipError_t launch_bwd_dkdv(const BwdParams& p, int io, int ct, int D, bool fused, hipStream_t st) {
+  return D == 64 ? kv_io<64>(p, io, ct, fused, st) : kv_io<128>(p, io, ct, false, st);
+}
+
+// ---------------------------------------------------------------------------
+// Packed RoPE table: out[0] = identity row, out[l + 1][p] = (cos, sin).
+// ---------------------------------------------------------------------------
+__global__ void rope_pack_kernel(const float* __restrict__ cosp, int64_t cs0, int64_t cs1,
+                                 const float* __restrict__ sinp, int64_t ss0, int64_t ss1,
+                                 int n_pos, int d2, float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)(n_pos + 1) * d2;
+  if (i >= total) return;
+  const int row = (int)(i / d2), pr = (int)(i - (int64_t)row * d2);
+  float c = 1.f, s = 0.f;
+  if (row > 0) {
+    c = cosp[(int64_t)(row - 1) * cs0 + pr * cs1];
+    s = sinp[(int64_t)(row - 1) * ss0 + pr * ss1];
+  }
+  out[2 * i] = c;
+  out[2 * i + 1] = s;
+}
+
+hipError_t launch_rope_pack(const float* cosp, int64_t cs0, int64_t cs1, const float* sinp,
+                            int64_t ss0, int64_t ss1, int n_pos, int d2, float* out,
+                            hipStream_t st) {
+  const int64_t total = (int64_t)(n_pos + 1) * d2;
+  const int grid = (int)((total + 255) / 256);
+  hipLaunchKernelGGL(rope_pack_kernel, dim3(grid), dim3(256), 0, st, cosp, cs0, cs1, sinp, ss0,
+                     ss1, n_pos, d2, out);
+  return hipGetLastError();
+}
+
+}  // namespace farope

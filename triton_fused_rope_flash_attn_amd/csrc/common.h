@@ -1,0 +1,248 @@
+// Device-side building blocks shared by the gfx950 attention kernels.
+//
+// Everything here is written for CDNA4 (gfx950): 64-lane wavefronts, the
+// v_mfma_f32_16x16x32_{bf16,f16} matrix instructions with fp32 accumulation,
+// and LDS tiles padded by 16 bytes per row so that 16-byte fragment reads
+// from 16 different rows land in disjoint bank groups.
+//
+// MFMA fragment convention used by every kernel (16x16x32 shape):
+//   lane = lr + 16*lg  (lr = lane & 15, lg = lane >> 4)
+//   A operand  (16 rows x 32 k):  lane supplies row lr, k = 8*lg .. 8*lg+7
+//   B operand  (32 k x 16 cols):  lane supplies col lr, k = 8*lg .. 8*lg+7
+//   C/D (16x16 fp32):             lane holds rows 4*lg .. 4*lg+3 of col lr
+// Only the pairing "A register e of lane group lg <-> B register e of lane
+// group lg" matters for a contraction, so the kernels are free to permute
+// which contraction index sits in which (lg, e) slot as long as both
+// operands use the same permutation.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace farope {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+typedef bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.69314718055994531f;
+
+// Element-type codes; identical to farope_dtype in include/farope.h.
+enum : int { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
+
+// ---------------------------------------------------------------------------
+// Global-memory I/O of the user tensors (fp32 / fp16 / bf16).
+// `vec` is decided on the host: the d-stride is 1 and every base/row offset
+// keeps the 16-byte alignment the vector path needs.  Otherwise the generic
+// strided path is used (stride 0 is legal, e.g. dO of o.sum()).
+// ---------------------------------------------------------------------------
+template <typename IO>
+__device__ __forceinline__ void load8(const IO* __restrict__ p, int64_t sd, bool vec,
+                                      float (&x)[8]) {
+  if (vec) {
+    if constexpr (sizeof(IO) == 4) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) { x[e] = a[e]; x[4 + e] = b[e]; }
+    } else {
+      typedef IO io8 __attribute__((ext_vector_type(8)));
+      const io8 a = *reinterpret_cast<const io8*>(p);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = (float)a[e];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = (float)p[e * sd];
+  }
+}
+
+template <typename IO>
+__device__ __forceinline__ void store4(IO* __restrict__ p, int64_t sd, bool vec,
+                                       const float (&x)[4]) {
+  if (vec) {
+    if constexpr (sizeof(IO) == 4) {
+      f32x4 a;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a[e] = x[e];
+      *reinterpret_cast<f32x4*>(p) = a;
+    } else {
+      typedef IO io4 __attribute__((ext_vector_type(4)));
+      io4 a;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a[e] = (IO)x[e];
+      *reinterpret_cast<io4*>(p) = a;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) p[e * sd] = (IO)x[e];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// RoPE.  The packed table is fp32 [(n_pos + 1)][D/2][2] = (cos, sin) per pair;
+// row 0 is the identity (cos 1, sin 0) and serves the CLS token, so token s
+// uses row s + (1 - has_cls) with no branch.
+// ---------------------------------------------------------------------------
+// Load (cos, sin) of pairs p0 .. p0+3 of one table row: cs = c0 s0 c1 s1 ...
+__device__ __forceinline__ void rope_load4(const float* __restrict__ tab, int row, int d2,
+                                           int p0, float (&cs)[8]) {
+  const f32x4* t = reinterpret_cast<const f32x4*>(tab + ((int64_t)row * d2 + p0) * 2);
+  const f32x4 a = t[0], b = t[1];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) { cs[e] = a[e]; cs[4 + e] = b[e]; }
+}
+
+// x-hat = R x for 4 adjacent pairs (2p, 2p+1):
+//   e' = e*c - o*s,  o' = o*c + e*s
+__device__ __forceinline__ void rope_rotate8(float (&x)[8], const float (&cs)[8]) {
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float e = x[2 * p], o = x[2 * p + 1], c = cs[2 * p], s = cs[2 * p + 1];
+    x[2 * p] = e * c - o * s;
+    x[2 * p + 1] = o * c + e * s;
+  }
+}
+
+// Gradient through the rotation: g = R^T g-hat for 2 adjacent pairs.
+//   ge = ge'*c + go'*s,  go = -ge'*s + go'*c
+__device__ __forceinline__ void rope_unrotate4(float (&g)[4], const float* __restrict__ tab,
+                                               int row, int d2, int p0) {
+  const f32x4 t = *reinterpret_cast<const f32x4*>(tab + ((int64_t)row * d2 + p0) * 2);
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const float e = g[2 * p], o = g[2 * p + 1], c = t[2 * p], s = t[2 * p + 1];
+    g[2 * p] = e * c + o * s;
+    g[2 * p + 1] = o * c - e * s;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Compute-type traits: how values are kept in LDS and fed to the MFMA unit.
+//   DT_BF16: bf16 storage, one v_mfma_f32_16x16x32_bf16 per product.
+//   DT_F16 : fp16 storage, one v_mfma_f32_16x16x32_f16 per product.
+//   DT_F32 : fp32 storage; each operand is split x = hi + lo (both bf16) and a
+//            product is hi*hi + hi*lo + lo*hi (three bf16 MFMAs), about 16
+//            mantissa bits, i.e. more than TF32.
+// ---------------------------------------------------------------------------
+template <int CT> struct Comp;
+
+template <> struct Comp<DT_BF16> {
+  typedef bf16 S;
+  struct Frag { bf16x8 v; };
+  static __device__ __forceinline__ Frag make(const float (&x)[8]) {
+    Frag f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f.v[e] = (bf16)x[e];
+    return f;
+  }
+  static __device__ __forceinline__ Frag zero() { Frag f; f.v = bf16x8{}; return f; }
+  static __device__ __forceinline__ Frag lds(const S* p) {
+    Frag f; f.v = *reinterpret_cast<const bf16x8*>(p); return f;
+  }
+  static __device__ __forceinline__ void put8(S* p, const float (&x)[8]) {
+    *reinterpret_cast<bf16x8*>(p) = make(x).v;
+  }
+  static __device__ __forceinline__ void put1(S* p, float x) { *p = (bf16)x; }
+  static __device__ __forceinline__ f32x4 mma(const Frag& a, const Frag& b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, c, 0, 0, 0);
+  }
+};
+
+template <> struct Comp<DT_F16> {
+  typedef f16 S;
+  struct Frag { f16x8 v; };
+  static __device__ __forceinline__ Frag make(const float (&x)[8]) {
+    Frag f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f.v[e] = (f16)x[e];
+    return f;
+  }
+  static __device__ __forceinline__ Frag zero() { Frag f; f.v = f16x8{}; return f; }
+  static __device__ __forceinline__ Frag lds(const S* p) {
+    Frag f; f.v = *reinterpret_cast<const f16x8*>(p); return f;
+  }
+  static __device__ __forceinline__ void put8(S* p, const float (&x)[8]) {
+    *reinterpret_cast<f16x8*>(p) = make(x).v;
+  }
+  static __device__ __forceinline__ void put1(S* p, float x) { *p = (f16)x; }
+  static __device__ __forceinline__ f32x4 mma(const Frag& a, const Frag& b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a.v, b.v, c, 0, 0, 0);
+  }
+};
+
+template <> struct Comp<DT_F32> {
+  typedef float S;
+  struct Frag { bf16x8 h, l; };
+  static __device__ __forceinline__ Frag make(const float (&x)[8]) {
+    Frag f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bf16 h = (bf16)x[e];
+      f.h[e] = h;
+      f.l[e] = (bf16)(x[e] - (float)h);
+    }
+    return f;
+  }
+  static __device__ __forceinline__ Frag zero() { Frag f; f.h = bf16x8{}; f.l = bf16x8{}; return f; }
+  static __device__ __forceinline__ Frag lds(const S* p) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { x[e] = a[e]; x[4 + e] = b[e]; }
+    return make(x);
+  }
+  static __device__ __forceinline__ void put8(S* p, const float (&x)[8]) {
+    f32x4 a, b;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { a[e] = x[e]; b[e] = x[4 + e]; }
+    *reinterpret_cast<f32x4*>(p) = a;
+    *reinterpret_cast<f32x4*>(p + 4) = b;
+  }
+  static __device__ __forceinline__ void put1(S* p, float x) { *p = x; }
+  static __device__ __forceinline__ f32x4 mma(const Frag& a, const Frag& b, f32x4 c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.l, b.h, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.l, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.h, c, 0, 0, 0);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Misc.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// Sum / max over the 4 lane groups that share one MFMA column (lanes
+// lr, lr+16, lr+32, lr+48).
+__device__ __forceinline__ float group4_sum(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+__device__ __forceinline__ float group4_max(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+// Workgroups are dispatched round-robin over MI355X's 8 XCDs (each with its
+// own L2).  Remap the linear workgroup id so that XCD x processes one
+// contiguous range of tiles; consecutive tiles (the q/kv blocks of one
+// (b, h) plane) then share that XCD's L2.  Bijective for any total T.
+__device__ __forceinline__ int xcd_remap(int L, int T) {
+  constexpr int X = 8;
+  const int per = T / X, rem = T % X;
+  const int x = L % X, i = L / X;
+  return x * per + (x < rem ? x : rem) + i;
+}
+
+__device__ __forceinline__ int round_up32(int x) { return (x + 31) & ~31; }
+
+}  // namespace farope

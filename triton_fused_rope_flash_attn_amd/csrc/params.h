@@ -1,0 +1,71 @@
+// Kernel argument blocks (passed by value) and the launcher declarations that
+// connect the C-ABI layer (api.hip) to the kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace farope {
+
+// One (b, h) plane of a [B, H, N, D] tensor starts at b*s[0] + h*s[1]
+// elements; row n, channel d at n*s[2] + d*s[3].
+struct FwdParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse;          // [B*H, N] fp32, natural-log log-sum-exp of the logits
+  int64_t sq[4], sk[4], sv[4], so[4];
+  const float* rope;   // packed (cos, sin) table [(n_pos + 1), D/2, 2]
+  int B, H, N, has_cls;
+  float scale_log2;    // softmax_scale * log2(e)
+  int vec_q, vec_k, vec_v, vec_o;
+  int n_blk;           // q blocks per plane
+};
+
+struct BwdParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;
+  const void* dout;
+  void* dq;
+  void* dk;
+  void* dv;
+  const float* lse;    // [B*H, N]
+  float* delta;        // [B*H, N]: rowsum(dO * O)
+  int64_t sq[4], sk[4], sv[4], so[4], sdo[4], sdq[4], sdk[4], sdv[4];
+  const float* rope;
+  int B, H, N, has_cls;
+  float scale;         // softmax_scale
+  float scale_log2;    // softmax_scale * log2(e)
+  int vec_q, vec_k, vec_v, vec_o, vec_do, vec_dq, vec_dk, vec_dv;
+  int n_blk;           // q blocks (dq kernel) or kv blocks (dk/dv kernel) per plane
+};
+
+// Launch shapes picked by the tile table (api.hip).
+enum FwdVariant : int {
+  FWD_PLANE = 0,    // whole (b,h) plane per workgroup, K-hat/V^T of the plane in LDS (N <= 256)
+  FWD_STREAM = 1,   // 64-row kv stages streamed through LDS (any N)
+};
+enum BwdVariant : int {
+  BWD_FUSED = 0,    // one workgroup per plane: dK, dV and dQ in one pass (N <= 256)
+  BWD_SPLIT = 1,    // dQ kernel (Q-outer, also writes delta) + dK/dV kernel (KV-outer)
+};
+
+// Launchers: return hipSuccess or the launch error.  io/ct are DT_* codes.
+hipError_t launch_fwd(const FwdParams& p, int io, int ct, int D, int variant, hipStream_t st);
+hipError_t launch_bwd_pre(const BwdParams& p, int io, int D, hipStream_t st);
+hipError_t launch_bwd_dq(const BwdParams& p, int io, int ct, int D, bool write_delta,
+                         hipStream_t st);
+hipError_t launch_bwd_dkdv(const BwdParams& p, int io, int ct, int D, bool fused, hipStream_t st);
+hipError_t launch_rope_pack(const float* cosp, int64_t cs0, int64_t cs1, const float* sinp,
+                            int64_t ss0, int64_t ss1, int n_pos, int d2, float* out,
+                            hipStream_t st);
+
+// Rows of q (fwd, dq) or kv (dk/dv) one workgroup covers, per variant.
+int fwd_block_rows(int D, int variant);
+int bwd_dq_block_rows(int D);
+int bwd_dkdv_block_rows(int D, bool fused);
+
+}  // namespace farope
