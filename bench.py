@@ -151,6 +151,32 @@ def time_torch_rocm(wl, steps, warmup):
             "what": "Python 2D RoPE (bf16) + F.scaled_dot_product_attention (flash/efficient), fwd+bwd"}
 
 
+def profile_run(wl, steps, warmup):
+    """Kernel launches only: `warmup + steps` x (fwd, bwd) and one calibration copy."""
+    import torch
+    from triton_fused_rope_flash_attn_amd import CosSinTable
+    from triton_fused_rope_flash_attn_amd import _lib
+
+    q, k, v, do = make_inputs(wl, "cuda")
+    B, H, N, D = q.shape
+    table = CosSinTable(100.0, wl["side"], wl["D"], device="cuda")
+    rope = table.packed()
+    scale = 1.0 / math.sqrt(D)
+    n_pos = N - int(wl["has_cls"])
+    for _ in range(warmup + steps):
+        o, lse = torch.ops.farope.attn_fwd(q, k, v, rope, n_pos, wl["has_cls"], scale, _lib.BF16)
+        torch.ops.farope.attn_bwd(do, q, k, v, o, lse, rope, n_pos, wl["has_cls"], scale, _lib.BF16)
+    # calibration: a plain copy reads and writes exactly 256 MiB each
+    src = torch.empty(128 * 1024 * 1024, dtype=torch.bfloat16, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    fb, bb = hbm_bytes(B, H, N, D)
+    print(json.dumps({"profile": wl["name"], "launches": warmup + steps, "fwd_alg_bytes": fb,
+                      "bwd_alg_bytes": bb, "calib_copy_bytes": 2 * src.numel() * 2}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -159,6 +185,9 @@ def main():
     ap.add_argument("--workload", default="vit_b", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-torch-baseline", action="store_true")
+    ap.add_argument("--profile", action="store_true",
+                    help="profiling mode for rocprofv3: only the fwd/bwd ops (warmup + steps) and one "
+                         "256 MiB device-to-device copy used to calibrate the HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -174,12 +203,17 @@ def main():
 
     wl = WORKLOADS[args.workload]
     dev = "cuda"
+    if args.profile:
+        profile_run(wl, args.steps, args.warmup)
+        return
     q, k, v, do = make_inputs(wl, dev)
     B, H, N, D = q.shape
     table = CosSinTable(100.0, wl["side"], wl["D"], device=dev)
     qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
 
     def step():
+        # gradients are consumed, not accumulated, as after zero_grad(set_to_none=True)
+        qq.grad = kk.grad = vv.grad = None
         o = sdpa_triton_fa_rope(qq, kk, vv, table, has_cls=wl["has_cls"])
         o.backward(do)
 

@@ -67,8 +67,8 @@ def _compare(tag, ours, ref, tol_max=TOL_MAX, tol_mean=TOL_MEAN, out_dtype=None,
     """Check max/mean abs error of ours vs ref.
 
     With out_dtype set, the bound is max(tolerance, FLOOR_MULT x the error of
-    storing ref in out_dtype) (see tests/cases.py).  `other` (torch bf16) is
-    only printed for comparison.
+    storing ref in out_dtype, the error of `other` = torch-ROCm bf16 SDPA +
+    RoPE on the same inputs) (see tests/cases.py).
     """
     names = ("O", "dQ", "dK", "dV")
     fails = []
@@ -78,13 +78,15 @@ def _compare(tag, ours, ref, tol_max=TOL_MAX, tol_mean=TOL_MEAN, out_dtype=None,
         mx, mn = errors(a, b)
         lim_max, lim_mean = tol_max, tol_mean
         extra = ""
+        omx = omn = 0.0
+        if other is not None:
+            omx, omn = errors(other[i], b)
         if out_dtype is not None and out_dtype != torch.float32:
             fmx, fmn = rounding_floor(b, out_dtype)
-            lim_max, lim_mean = allowed(fmx, fmn)
+            lim_max, lim_mean = allowed(fmx, fmn, omx, omn)
             lim_max, lim_mean = max(lim_max, tol_max), max(lim_mean, tol_mean)
             extra = f" | storage floor max {fmx:.3e} mean {fmn:.3e}"
         if other is not None:
-            omx, omn = errors(other[i], b)
             extra += f" | torch-bf16 max {omx:.3e} mean {omn:.3e}"
         _say(f"[{tag}] {name}: max_abs_err={mx:.3e} mean_abs_err={mn:.3e} (bound {lim_max:.2e}/{lim_mean:.2e}){extra}")
         if mx > lim_max or mn > lim_mean:
@@ -159,7 +161,8 @@ def test_ragged_and_variant_shapes(side, has_cls, D):
     table = CosSinTable(ROPE_BASE, side, D, device=DEV)
     ours = _run_ours(q, k, v, do, table, has_cls)
     ref = _ref(q, k, v, do, table, has_cls)
-    _compare(f"side{side}-cls{int(has_cls)}-D{D}", ours, ref, out_dtype=torch.bfloat16)
+    other = _torch_bf16(q, k, v, do, table, has_cls)
+    _compare(f"side{side}-cls{int(has_cls)}-D{D}", ours, ref, out_dtype=torch.bfloat16, other=other)
 
 
 def test_strided_qkv_views():
@@ -197,8 +200,10 @@ def test_stride0_dout_from_sum():
     q, k, v, _ = make_inputs(cfg, DEV)
     table = CosSinTable(ROPE_BASE, 14, 64, device=DEV)
     ours = _run_ours(q, k, v, None, table, True, sum_loss=True)
-    ref = _ref(q, k, v, torch.ones_like(q, dtype=torch.float32), table, True)
-    _compare("stride0-dO", ours, ref, out_dtype=torch.bfloat16)
+    ones = torch.ones_like(q, dtype=torch.float32)
+    ref = _ref(q, k, v, ones, table, True)
+    other = _torch_bf16(q, k, v, ones.to(q.dtype), table, True)
+    _compare("stride0-dO", ours, ref, out_dtype=torch.bfloat16, other=other)
 
 
 def test_triton_attention_apply_signature():

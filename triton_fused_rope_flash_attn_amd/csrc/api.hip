@@ -48,7 +48,11 @@ void copy4(int64_t dst[4], const int64_t src[4]) {
 }
 
 bool fwd_plane(const farope_attn_desc* d) { return d->head_dim == 64 && d->seq_len <= kPlaneMaxN; }
-bool bwd_fused(const farope_attn_desc* d) { return d->head_dim == 64 && d->seq_len <= kPlaneMaxN; }
+// The one-pass backward keeps bf16/fp16 tiles of the plane in LDS; fp32
+// compute (twice the bytes) takes the split path.
+bool bwd_fused(const farope_attn_desc* d) {
+  return d->head_dim == 64 && d->seq_len <= bwd_fused_rows() && d->compute_dtype != FAROPE_F32;
+}
 
 int cdiv(int a, int b) { return (a + b - 1) / b; }
 
@@ -119,11 +123,11 @@ int farope_tile_config(const farope_attn_desc* desc, int32_t which, int32_t out[
     out[0] = var;
     out[1] = rows;
     out[2] = cdiv(N, rows);
-    out[3] = var == FWD_PLANE ? 512 : 256;
+    out[3] = 256;
   } else {
     const bool fu = bwd_fused(desc);
     out[0] = fu ? BWD_FUSED : BWD_SPLIT;
-    out[1] = fu ? bwd_dkdv_block_rows(D, true) : bwd_dkdv_block_rows(D, false);
+    out[1] = fu ? bwd_fused_rows() : bwd_dkdv_block_rows(D);
     out[2] = cdiv(N, out[1]);
     out[3] = fu ? 512 : 256;
   }
@@ -210,8 +214,8 @@ int farope_attn_bwd_dk_dv(const farope_attn_desc* desc, const void* q, const int
   p.vec_do = vec_ok(dout, dout_stride, es);
   p.vec_dk = vec_ok(dk, dk_stride, es);
   p.vec_dv = vec_ok(dv, dv_stride, es);
-  p.n_blk = cdiv(p.N, bwd_dkdv_block_rows(desc->head_dim, false));
-  return launch_rc(launch_bwd_dkdv(p, desc->io_dtype, desc->compute_dtype, desc->head_dim, false,
+  p.n_blk = cdiv(p.N, bwd_dkdv_block_rows(desc->head_dim));
+  return launch_rc(launch_bwd_dkdv(p, desc->io_dtype, desc->compute_dtype, desc->head_dim,
                                    static_cast<hipStream_t>(stream)));
 }
 
@@ -291,12 +295,12 @@ int farope_attn_bwd(const farope_attn_desc* desc, const void* q, const int64_t q
   const int D = desc->head_dim;
   if (fused) {
     p.n_blk = 1;
-    return launch_rc(launch_bwd_dkdv(p, desc->io_dtype, desc->compute_dtype, D, true, st));
+    return launch_rc(launch_bwd_fused(p, desc->io_dtype, desc->compute_dtype, st));
   }
   p.n_blk = cdiv(p.N, bwd_dq_block_rows(D));
   FAROPE_TRY(launch_rc(launch_bwd_dq(p, desc->io_dtype, desc->compute_dtype, D, true, st)));
-  p.n_blk = cdiv(p.N, bwd_dkdv_block_rows(D, false));
-  return launch_rc(launch_bwd_dkdv(p, desc->io_dtype, desc->compute_dtype, D, false, st));
+  p.n_blk = cdiv(p.N, bwd_dkdv_block_rows(D));
+  return launch_rc(launch_bwd_dkdv(p, desc->io_dtype, desc->compute_dtype, D, st));
 }
 
 }  // extern "C"

@@ -14,11 +14,8 @@
 //    so P and dS land directly in the B-operand layout of
 //    dV^T += dO^T P and dK-hat^T += Q-hat^T dS; dO^T and Q-hat^T are staged
 //    transposed in LDS once per query stage and shared by all waves.
-//  * Fused variant (N <= 256): one workgroup owns a whole (b, h) plane, so
-//    all keys of a query stage are on-chip.  dS of the stage is written to
-//    LDS and the same workgroup finishes dQ-hat^T = K-hat^T dS^T for that
-//    stage before moving on: S, P and dP are computed once, delta is formed
-//    while staging O and dO, and Q, K, V, O, dO are each read from HBM once.
+//  * For planes that fit on chip the one-pass kernel in bwd_fused.hip is
+//    used instead; the kernels here serve any N and head_dim.
 //  * dQ kernel (Q-outer, any N): logits transposed as in the forward pass;
 //    dS^T lands in the B-operand layout of dQ-hat^T += K-hat^T dS^T.  It
 //    can produce delta itself, so the split path needs no separate
@@ -238,10 +235,9 @@ bwd_dq_kernel(const BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// dK/dV kernel (KV-outer); FUSED additionally produces dQ (whole plane per
-// workgroup, NKV >= N).
+// dK/dV kernel (KV-outer).
 // ---------------------------------------------------------------------------
-template <typename IO, int CT, int D, int NW, int KT, int QS, bool FUSED>
+template <typename IO, int CT, int D, int NW, int KT, int QS>
 __global__ void __launch_bounds__(NW * 64)
 bwd_dkdv_kernel(const BwdParams p) {
   using C = Comp<CT>;
@@ -253,8 +249,6 @@ bwd_dkdv_kernel(const BwdParams p) {
   constexpr int NT = NW * 64, CPR = D / 8;
   constexpr int ITER = (QS * CPR + NT - 1) / NT;
   constexpr int KROWS = NW * KT * 16;           // kv rows per workgroup
-  constexpr int LDKT = KROWS + PADE;            // fused: K-hat^T / dS row pitch
-  constexpr int KITER = (KROWS * CPR + NT - 1) / NT;
 
   __shared__ __attribute__((aligned(16))) S sQ[QS * LDQ];
   __shared__ __attribute__((aligned(16))) S sQt[D * LDT];
@@ -262,8 +256,6 @@ bwd_dkdv_kernel(const BwdParams p) {
   __shared__ __attribute__((aligned(16))) S sGt[D * LDT];
   __shared__ __attribute__((aligned(16))) float sL2[QS];
   __shared__ __attribute__((aligned(16))) float sDl[QS];
-  __shared__ __attribute__((aligned(16))) S sKt[FUSED ? D * LDKT : 8];
-  __shared__ __attribute__((aligned(16))) S sdS[FUSED ? QS * LDKT : 8];
 
   const int N = p.N;
   const int tile = xcd_remap(blockIdx.x, gridDim.x);
@@ -273,9 +265,7 @@ bwd_dkdv_kernel(const BwdParams p) {
   const IO* __restrict__ Q = static_cast<const IO*>(p.q) + bb * p.sq[0] + hh * p.sq[1];
   const IO* __restrict__ K = static_cast<const IO*>(p.k) + bb * p.sk[0] + hh * p.sk[1];
   const IO* __restrict__ V = static_cast<const IO*>(p.v) + bb * p.sv[0] + hh * p.sv[1];
-  const IO* __restrict__ O = static_cast<const IO*>(p.o) + bb * p.so[0] + hh * p.so[1];
   const IO* __restrict__ G = static_cast<const IO*>(p.dout) + bb * p.sdo[0] + hh * p.sdo[1];
-  IO* __restrict__ dQ = static_cast<IO*>(p.dq) + bb * p.sdq[0] + hh * p.sdq[1];
   IO* __restrict__ dK = static_cast<IO*>(p.dk) + bb * p.sdk[0] + hh * p.sdk[1];
   IO* __restrict__ dV = static_cast<IO*>(p.dv) + bb * p.sdv[0] + hh * p.sdv[1];
   const float* __restrict__ tab = p.rope;
@@ -317,41 +307,12 @@ bwd_dkdv_kernel(const BwdParams p) {
 #pragma unroll
     for (int d = 0; d < DT; ++d) dvacc[u][d] = dkacc[u][d] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int nkv32 = round_up32(N);   // fused: key columns held in sKt / sdS
-  if constexpr (FUSED) {
-    // K-hat^T of the whole plane (zero beyond N) and a zeroed dS buffer.
-    float xk[KITER][8], cs[KITER][8];
-#pragma unroll
-    for (int it = 0; it < KITER; ++it) {
-      const int c = tid + it * NT;
-      const int r = c / CPR, cc = c - r * CPR;
-      if (c < nkv32 * CPR && r < N) {
-        load8(K + r * p.sk[2] + 8 * cc * p.sk[3], p.sk[3], p.vec_k, xk[it]);
-        rope_load4(tab, r + shift, D2, 4 * cc, cs[it]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) { xk[it][e] = 0.f; cs[it][e] = 0.f; }
-      }
-    }
-#pragma unroll
-    for (int it = 0; it < KITER; ++it) {
-      const int c = tid + it * NT;
-      const int r = c / CPR, cc = c - r * CPR;
-      if (c < nkv32 * CPR) {
-        rope_rotate8(xk[it], cs[it]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) C::put1(&sKt[(8 * cc + e) * LDKT + r], xk[it][e]);
-      }
-    }
-    for (int i = tid; i < QS * LDKT; i += NT) C::put1(&sdS[i], 0.f);
-  }
-
   for (int qb = 0; qb < N; qb += QS) {
     const int rows = min(QS, round_up32(N - qb));
     __syncthreads();
     // ---- stage Q-hat, Q-hat^T, dO, dO^T (+ delta, LSE) for this q stage ----
     {
-      float xq[ITER][8], xg[ITER][8], cs[ITER][8], xo[ITER][8];
+      float xq[ITER][8], xg[ITER][8], cs[ITER][8];
 #pragma unroll
       for (int it = 0; it < ITER; ++it) {
         const int c = tid + it * NT;
@@ -360,25 +321,15 @@ bwd_dkdv_kernel(const BwdParams p) {
           load8(Q + gr * p.sq[2] + 8 * cc * p.sq[3], p.sq[3], p.vec_q, xq[it]);
           load8(G + gr * p.sdo[2] + 8 * cc * p.sdo[3], p.sdo[3], p.vec_do, xg[it]);
           rope_load4(tab, gr + shift, D2, 4 * cc, cs[it]);
-          if (FUSED) load8(O + gr * p.so[2] + 8 * cc * p.so[3], p.so[3], p.vec_o, xo[it]);
         } else {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) { xq[it][e] = xg[it][e] = cs[it][e] = xo[it][e] = 0.f; }
+          for (int e = 0; e < 8; ++e) { xq[it][e] = xg[it][e] = cs[it][e] = 0.f; }
         }
       }
 #pragma unroll
       for (int it = 0; it < ITER; ++it) {
         const int c = tid + it * NT;
         const int r = c / CPR, cc = c - r * CPR;
-        if (FUSED) {
-          // delta for row r: the CPR chunks of a row sit in consecutive lanes.
-          float dsum = 0.f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) dsum += xg[it][e] * xo[it][e];
-#pragma unroll
-          for (int m = 1; m < CPR; m <<= 1) dsum += __shfl_xor(dsum, m);
-          if (c < rows * CPR && cc == 0) sDl[r] = dsum;
-        }
         if (c < rows * CPR) {
           rope_rotate8(xq[it], cs[it]);
           C::put8(&sQ[r * LDQ + 8 * cc], xq[it]);
@@ -393,7 +344,7 @@ bwd_dkdv_kernel(const BwdParams p) {
       for (int r = tid; r < rows; r += NT) {
         const int gr = qb + r;
         sL2[r] = gr < N ? p.lse[prow + gr] * kLog2e : INFINITY;
-        if (!FUSED) sDl[r] = gr < N ? p.delta[prow + gr] : 0.f;
+        sDl[r] = gr < N ? p.delta[prow + gr] : 0.f;
       }
     }
     __syncthreads();
@@ -445,35 +396,9 @@ bwd_dkdv_kernel(const BwdParams p) {
           const Frag aq = C::lds(&sQt[(16 * d + lr) * LDT + 32 * j + 8 * lg]);
           dkacc[u][d] = C::mma(aq, dsf, dkacc[u][d]);
         }
-        if constexpr (FUSED) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) C::put1(&sdS[(32 * j + 8 * lg + e) * LDKT + kv0 + lr], dsv[e]);
-        }
       }
     }
 
-    if constexpr (FUSED) {
-      __syncthreads();
-      // dQ-hat^T[d, q] = sum_kv K-hat^T[d, kv] dS^T[kv, q] for this stage.
-      const int jobs = (rows / 16) * DT;
-      for (int job = wave; job < jobs; job += NW) {
-        const int qs = job / DT, d = job - qs * DT;
-        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-        for (int jj = 0; jj < nkv32 / 32; ++jj) {
-          const Frag a = C::lds(&sKt[(16 * d + lr) * LDKT + 32 * jj + 8 * lg]);
-          const Frag b = C::lds(&sdS[(16 * qs + lr) * LDKT + 32 * jj + 8 * lg]);
-          acc = C::mma(a, b, acc);
-        }
-        const int row = qb + 16 * qs + lr;
-        if (row < N) {
-          float g4[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) g4[r] = acc[r] * p.scale;
-          rope_unrotate4(g4, tab, row + shift, D2, 8 * d + 2 * lg);
-          store4(dQ + row * p.sdq[2] + (16 * d + 4 * lg) * p.sdq[3], p.sdq[3], p.vec_dq, g4);
-        }
-      }
-    }
   }
 
   // ---- epilogue: lane holds dV / dK-hat of kv row kv0 + lr, channels 16d + 4lg + (0..3) ----
@@ -501,23 +426,19 @@ template <int D> struct BwdShape;
 template <> struct BwdShape<64> {
   static constexpr int DQ_NW = 4, DQ_QT = 2, DQ_KVS = 64;
   static constexpr int KV_NW = 4, KV_KT = 2, KV_QS = 64;
-  static constexpr int FU_NW = 8, FU_KT = 2, FU_QS = 32;   // 256 kv rows per workgroup
 };
 template <> struct BwdShape<128> {
   static constexpr int DQ_NW = 4, DQ_QT = 1, DQ_KVS = 64;
   static constexpr int KV_NW = 4, KV_KT = 1, KV_QS = 64;
-  static constexpr int FU_NW = 8, FU_KT = 1, FU_QS = 32;   // unused: D=128 uses the split path
 };
 
 int bwd_dq_block_rows(int D) {
   return D == 64 ? BwdShape<64>::DQ_NW * BwdShape<64>::DQ_QT * 16
                  : BwdShape<128>::DQ_NW * BwdShape<128>::DQ_QT * 16;
 }
-int bwd_dkdv_block_rows(int D, bool fused) {
-  if (D == 64)
-    return fused ? BwdShape<64>::FU_NW * BwdShape<64>::FU_KT * 16
-                 : BwdShape<64>::KV_NW * BwdShape<64>::KV_KT * 16;
-  return BwdShape<128>::KV_NW * BwdShape<128>::KV_KT * 16;
+int bwd_dkdv_block_rows(int D) {
+  return D == 64 ? BwdShape<64>::KV_NW * BwdShape<64>::KV_KT * 16
+                 : BwdShape<128>::KV_NW * BwdShape<128>::KV_KT * 16;
 }
 
 template <typename IO, int D>
@@ -558,15 +479,11 @@ static hipError_t dq_launch(const BwdParams& p, bool write_delta, hipStream_t st
 }
 
 template <typename IO, int CT, int D>
-static hipError_t dkdv_launch(const BwdParams& p, bool fused, hipStream_t st) {
+static hipError_t dkdv_launch(const BwdParams& p, hipStream_t st) {
   using SH = BwdShape<D>;
   const int grid = p.B * p.H * p.n_blk;
-  if (fused && D == 64)
-    hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::FU_NW, SH::FU_KT, SH::FU_QS, true>),
-                       dim3(grid), dim3(SH::FU_NW * 64), 0, st, p);
-  else
-    hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS, false>),
-                       dim3(grid), dim3(SH::KV_NW * 64), 0, st, p);
+  hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS>), dim3(grid),
+                     dim3(SH::KV_NW * 64), 0, st, p);
   return hipGetLastError();
 }
 
@@ -592,23 +509,23 @@ hipError_t launch_bwd_dq(const BwdParams& p, int io, int ct, int D, bool write_d
 }
 
 template <typename IO, int D>
-static hipError_t kv_ct(const BwdParams& p, int ct, bool fu, hipStream_t st) {
+static hipError_t kv_ct(const BwdParams& p, int ct, hipStream_t st) {
   switch (ct) {
-    case DT_BF16: return dkdv_launch<IO, DT_BF16, D>(p, fu, st);
-    case DT_F16: return dkdv_launch<IO, DT_F16, D>(p, fu, st);
-    default: return dkdv_launch<IO, DT_F32, D>(p, fu, st);
+    case DT_BF16: return dkdv_launch<IO, DT_BF16, D>(p, st);
+    case DT_F16: return dkdv_launch<IO, DT_F16, D>(p, st);
+    default: return dkdv_launch<IO, DT_F32, D>(p, st);
   }
 }
 template <int D>
-static hipError_t kv_io(const BwdParams& p, int io, int ct, bool fu, hipStream_t st) {
+static hipError_t kv_io(const BwdParams& p, int io, int ct, hipStream_t st) {
   switch (io) {
-    case DT_BF16: return kv_ct<bf16, D>(p, ct, fu, st);
-    case DT_F16: return kv_ct<f16, D>(p, ct, fu, st);
-    default: return kv_ct<float, D>(p, ct, fu, st);
+    case DT_BF16: return kv_ct<bf16, D>(p, ct, st);
+    case DT_F16: return kv_ct<f16, D>(p, ct, st);
+    default: return kv_ct<float, D>(p, ct, st);
   }
 }
-hipError_t launch_bwd_dkdv(const BwdParams& p, int io, int ct, int D, bool fused, hipStream_t st) {
-  return D == 64 ? kv_io<64>(p, io, ct, fused, st) : kv_io<128>(p, io, ct, false, st);
+hipError_t launch_bwd_dkdv(const BwdParams& p, int io, int ct, int D, hipStream_t st) {
+  return D == 64 ? kv_io<64>(p, io, ct, st) : kv_io<128>(p, io, ct, st);
 }
 
 // ---------------------------------------------------------------------------

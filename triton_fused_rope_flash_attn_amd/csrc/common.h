@@ -62,6 +62,39 @@ __device__ __forceinline__ void load8(const IO* __restrict__ p, int64_t sd, bool
   }
 }
 
+// Raw 8-element row segment kept in its I/O type while a load is in flight
+// (prefetch registers: 16 bytes for 2-byte types).
+template <typename IO> struct Raw8 {
+  typedef IO vec __attribute__((ext_vector_type(8)));
+  vec v;
+};
+
+template <typename IO>
+__device__ __forceinline__ Raw8<IO> load_raw8(const IO* __restrict__ p, int64_t sd, bool vec) {
+  Raw8<IO> r;
+  if (vec) {
+    r.v = *reinterpret_cast<const typename Raw8<IO>::vec*>(p);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r.v[e] = p[e * sd];
+  }
+  return r;
+}
+
+template <typename IO>
+__device__ __forceinline__ Raw8<IO> zero_raw8() {
+  Raw8<IO> r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r.v[e] = (IO)0.f;
+  return r;
+}
+
+template <typename IO>
+__device__ __forceinline__ void unpack8(const Raw8<IO>& r, float (&x)[8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = (float)r.v[e];
+}
+
 template <typename IO>
 __device__ __forceinline__ void store4(IO* __restrict__ p, int64_t sd, bool vec,
                                        const float (&x)[4]) {
@@ -142,6 +175,17 @@ template <> struct Comp<DT_BF16> {
     return f;
   }
   static __device__ __forceinline__ Frag zero() { Frag f; f.v = bf16x8{}; return f; }
+  static __device__ __forceinline__ void set(Frag& f, int e, float x) { f.v[e] = (bf16)x; }
+  // elements 2w, 2w+1 from two floats (one packed conversion)
+  static __device__ __forceinline__ void set2(Frag& f, int w, float a, float b) {
+    typedef bf16 v2 __attribute__((ext_vector_type(2)));
+    v2 t;
+    t[0] = (bf16)a;
+    t[1] = (bf16)b;
+    f.v[2 * w] = t[0];
+    f.v[2 * w + 1] = t[1];
+  }
+  static __device__ __forceinline__ void put_elem(S* p, const Frag& f, int e) { *p = f.v[e]; }
   static __device__ __forceinline__ Frag lds(const S* p) {
     Frag f; f.v = *reinterpret_cast<const bf16x8*>(p); return f;
   }
@@ -164,6 +208,16 @@ template <> struct Comp<DT_F16> {
     return f;
   }
   static __device__ __forceinline__ Frag zero() { Frag f; f.v = f16x8{}; return f; }
+  static __device__ __forceinline__ void set(Frag& f, int e, float x) { f.v[e] = (f16)x; }
+  static __device__ __forceinline__ void set2(Frag& f, int w, float a, float b) {
+    typedef f16 v2 __attribute__((ext_vector_type(2)));
+    v2 t;
+    t[0] = (f16)a;
+    t[1] = (f16)b;
+    f.v[2 * w] = t[0];
+    f.v[2 * w + 1] = t[1];
+  }
+  static __device__ __forceinline__ void put_elem(S* p, const Frag& f, int e) { *p = f.v[e]; }
   static __device__ __forceinline__ Frag lds(const S* p) {
     Frag f; f.v = *reinterpret_cast<const f16x8*>(p); return f;
   }
@@ -190,6 +244,18 @@ template <> struct Comp<DT_F32> {
     return f;
   }
   static __device__ __forceinline__ Frag zero() { Frag f; f.h = bf16x8{}; f.l = bf16x8{}; return f; }
+  static __device__ __forceinline__ void set(Frag& f, int e, float x) {
+    const bf16 h = (bf16)x;
+    f.h[e] = h;
+    f.l[e] = (bf16)(x - (float)h);
+  }
+  static __device__ __forceinline__ void set2(Frag& f, int w, float a, float b) {
+    set(f, 2 * w, a);
+    set(f, 2 * w + 1, b);
+  }
+  static __device__ __forceinline__ void put_elem(S* p, const Frag& f, int e) {
+    *p = (float)f.h[e] + (float)f.l[e];
+  }
   static __device__ __forceinline__ Frag lds(const S* p) {
     const f32x4 a = *reinterpret_cast<const f32x4*>(p);
     const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);

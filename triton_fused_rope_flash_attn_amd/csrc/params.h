@@ -45,8 +45,8 @@ struct BwdParams {
 
 // Launch shapes picked by the tile table (api.hip).
 enum FwdVariant : int {
-  FWD_PLANE = 0,    // whole (b,h) plane per workgroup, K-hat/V^T of the plane in LDS (N <= 256)
-  FWD_STREAM = 1,   // 64-row kv stages streamed through LDS (any N)
+  FWD_PLANE = 0,    // one workgroup per (b,h) plane, K-hat/V^T of the plane kept in LDS (N <= 256)
+  FWD_STREAM = 1,   // kv chunks streamed through a double-buffered LDS ring (any N)
 };
 enum BwdVariant : int {
   BWD_FUSED = 0,    // one workgroup per plane: dK, dV and dQ in one pass (N <= 256)
@@ -58,7 +58,9 @@ hipError_t launch_fwd(const FwdParams& p, int io, int ct, int D, int variant, hi
 hipError_t launch_bwd_pre(const BwdParams& p, int io, int D, hipStream_t st);
 hipError_t launch_bwd_dq(const BwdParams& p, int io, int ct, int D, bool write_delta,
                          hipStream_t st);
-hipError_t launch_bwd_dkdv(const BwdParams& p, int io, int ct, int D, bool fused, hipStream_t st);
+hipError_t launch_bwd_dkdv(const BwdParams& p, int io, int ct, int D, hipStream_t st);
+// One-pass backward (bwd_fused.hip): D = 64, N <= bwd_fused_rows(), ct bf16 or fp16.
+hipError_t launch_bwd_fused(const BwdParams& p, int io, int ct, hipStream_t st);
 hipError_t launch_rope_pack(const float* cosp, int64_t cs0, int64_t cs1, const float* sinp,
                             int64_t ss0, int64_t ss1, int n_pos, int d2, float* out,
                             hipStream_t st);
@@ -66,6 +68,7 @@ hipError_t launch_rope_pack(const float* cosp, int64_t cs0, int64_t cs1, const f
 // Rows of q (fwd, dq) or kv (dk/dv) one workgroup covers, per variant.
 int fwd_block_rows(int D, int variant);
 int bwd_dq_block_rows(int D);
-int bwd_dkdv_block_rows(int D, bool fused);
+int bwd_dkdv_block_rows(int D);
+int bwd_fused_rows();
 
 }  // namespace farope
