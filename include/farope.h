@@ -142,9 +142,10 @@ int farope_attn_bwd(const farope_attn_desc* desc,
 /*
  * Tile table query (replaces the reference's triton.autotune configs,
  * FA:76-90, FA:318-324, FA:359-373, FA:693-707).  which: 0 = forward,
- * 1 = backward.  out[0] = variant (fwd: 0 plane-resident, 1 streamed;
- * bwd: 0 fused, 1 split), out[1] = rows per workgroup, out[2] = workgroups
- * per (b, h) plane, out[3] = threads per workgroup.
+ * 1 = backward.  out[0] = variant (fwd: 0 = persistent pipelined kernel;
+ * bwd: 0 fused, 1 split), out[1] = query (fwd) or key (bwd) rows per work
+ * item, out[2] = work items per (b, h) plane, out[3] = threads per
+ * workgroup.
  */
 int farope_tile_config(const farope_attn_desc* desc, int32_t which, int32_t out[4]);
 

@@ -64,17 +64,22 @@ def test_rope_packed_elems(lib):
 
 
 @pytest.mark.parametrize(
-    "N,D,has_cls,fwd_var,bwd_var",
-    [(197, 64, 1, 0, 0), (256, 64, 0, 0, 0), (257, 64, 1, 1, 1), (1025, 128, 1, 1, 1), (197, 128, 1, 1, 1)],
+    "N,D,has_cls,fwd_items,bwd_var",
+    [(197, 64, 1, 1, 0), (256, 64, 0, 1, 0), (257, 64, 1, 2, 1), (1025, 128, 1, 9, 1), (197, 128, 1, 2, 1)],
 )
-def test_tile_table(lib, N, D, has_cls, fwd_var, bwd_var):
+def test_tile_table(lib, N, D, has_cls, fwd_items, bwd_var):
     desc = _lib.make_desc(8, 12, N, D, N - has_cls, has_cls, _lib.BF16, _lib.BF16, D ** -0.5)
     f = _lib.tile_config(desc, 0)
     b = _lib.tile_config(desc, 1)
-    assert f[0] == fwd_var and b[0] == bwd_var
+    assert f[0] == 0 and f[2] == fwd_items and b[0] == bwd_var
     assert f[1] * f[2] >= N and b[1] * b[2] >= N      # blocks cover the sequence
     assert (f[2] - 1) * f[1] < N and (b[2] - 1) * b[1] < N  # and no empty block
     assert f[3] % 64 == 0 and b[3] % 64 == 0
+
+
+def test_fp32_compute_takes_split_backward(lib):
+    desc = _lib.make_desc(8, 12, 197, 64, 196, 1, _lib.F32, _lib.F32, 0.125)
+    assert _lib.tile_config(desc, 1)[0] == 1
 
 
 def _call_fwd(lib, desc, q=16, lse=16, rope=16):

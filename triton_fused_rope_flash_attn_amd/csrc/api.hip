@@ -4,9 +4,41 @@
 
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+#include <unordered_map>
+
 #include "params.h"
 
 using namespace farope;
+
+namespace farope {
+
+// Resident-capacity query for persistent kernels, cached per (device, kernel).
+int persistent_grid(const void* kernel, int block_threads, int items) {
+  static std::mutex mu;
+  static std::unordered_map<uint64_t, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  const uint64_t key = (reinterpret_cast<uint64_t>(kernel) << 8) ^ (uint64_t)(dev & 0xff);
+  int cap = 0;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) cap = it->second;
+  }
+  if (cap == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block_threads, 0) != hipSuccess)
+      return -1;
+    cap = cus * (per_cu > 0 ? per_cu : 1);
+    std::lock_guard<std::mutex> lock(mu);
+    cache[key] = cap;
+  }
+  return items < cap ? items : cap;
+}
+
+}  // namespace farope
 
 namespace {
 
@@ -47,7 +79,6 @@ void copy4(int64_t dst[4], const int64_t src[4]) {
   for (int i = 0; i < 4; ++i) dst[i] = src[i];
 }
 
-bool fwd_plane(const farope_attn_desc* d) { return d->head_dim == 64 && d->seq_len <= kPlaneMaxN; }
 // The one-pass backward keeps bf16/fp16 tiles of the plane in LDS; fp32
 // compute (twice the bytes) takes the split path.
 bool bwd_fused(const farope_attn_desc* d) {
@@ -118,12 +149,11 @@ int farope_tile_config(const farope_attn_desc* desc, int32_t which, int32_t out[
   if (!out) return FAROPE_ERR_NULL;
   const int D = desc->head_dim, N = desc->seq_len;
   if (which == 0) {
-    const int var = fwd_plane(desc) ? FWD_PLANE : FWD_STREAM;
-    const int rows = fwd_block_rows(D, var);
-    out[0] = var;
+    const int rows = fwd_block_rows(D);
+    out[0] = 0;
     out[1] = rows;
     out[2] = cdiv(N, rows);
-    out[3] = 256;
+    out[3] = fwd_threads(D);
   } else {
     const bool fu = bwd_fused(desc);
     out[0] = fu ? BWD_FUSED : BWD_SPLIT;
@@ -158,9 +188,9 @@ int farope_attn_fwd(const farope_attn_desc* desc, const void* q, const int64_t q
   p.vec_k = vec_ok(k, k_stride, es);
   p.vec_v = vec_ok(v, v_stride, es);
   p.vec_o = vec_ok(o, o_stride, es);
-  const int var = fwd_plane(desc) ? FWD_PLANE : FWD_STREAM;
-  p.n_blk = cdiv(p.N, fwd_block_rows(desc->head_dim, var));
-  return launch_rc(launch_fwd(p, desc->io_dtype, desc->compute_dtype, desc->head_dim, var,
+  p.n_blk = cdiv(p.N, fwd_block_rows(desc->head_dim));
+  p.n_items = p.B * p.H * p.n_blk;
+  return launch_rc(launch_fwd(p, desc->io_dtype, desc->compute_dtype, desc->head_dim,
                               static_cast<hipStream_t>(stream)));
 }
 

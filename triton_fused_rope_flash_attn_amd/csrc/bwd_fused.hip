@@ -59,7 +59,9 @@ __device__ __forceinline__ int rperm(int r) {
   return (r & ~31) | ((r & 4) << 2) | ((r & 24) >> 1) | (r & 3);
 }
 
-template <typename IO, int CT, int D, int NW, int KT, int QS>
+// VEC: every tensor of the call allows 16-byte vector access (decided on the
+// host); the generic instantiation gathers element by element instead.
+template <typename IO, int CT, int D, int NW, int KT, int QS, bool VEC>
 __global__ void __launch_bounds__(NW * 64)
 bwd_fused_kernel(const BwdParams p) {
   using C = Comp<CT>;
@@ -88,6 +90,9 @@ bwd_fused_kernel(const BwdParams p) {
   __shared__ __attribute__((aligned(16))) S sdS[QS * LDKT];
 
   const int N = p.N;
+  const bool vec_q = VEC || p.vec_q, vec_k = VEC || p.vec_k, vec_v = VEC || p.vec_v;
+  const bool vec_o = VEC || p.vec_o, vec_do = VEC || p.vec_do, vec_dq = VEC || p.vec_dq;
+  const bool vec_dk = VEC || p.vec_dk, vec_dv = VEC || p.vec_dv;
   const int plane = xcd_remap(blockIdx.x, gridDim.x);
   const int bb = plane / p.H, hh = plane - bb * p.H;
   const IO* __restrict__ Q = static_cast<const IO*>(p.q) + bb * p.sq[0] + hh * p.sq[1];
@@ -130,7 +135,7 @@ bwd_fused_kernel(const BwdParams p) {
       if (q_thread) {
         float cs[8];
         if (gr < N) {
-          put_raw(x, load_raw8(Q + gr * p.sq[2] + 8 * scc * p.sq[3], p.sq[3], p.vec_q));
+          put_raw(x, load_raw8(Q + gr * p.sq[2] + 8 * scc * p.sq[3], p.sq[3], vec_q));
           rope_load4(tab, gr + shift, D2, 4 * scc, cs);
         } else {
           put_raw(x, zero_raw8<IO>());
@@ -140,8 +145,8 @@ bwd_fused_kernel(const BwdParams p) {
         __builtin_memcpy(&pre[2 * W + 8 * x], cs, sizeof(cs));
       } else {
         if (gr < N) {
-          put_raw(x, load_raw8(G + gr * p.sdo[2] + 8 * scc * p.sdo[3], p.sdo[3], p.vec_do));
-          put_raw(2 + x, load_raw8(O + gr * p.so[2] + 8 * scc * p.so[3], p.so[3], p.vec_o));
+          put_raw(x, load_raw8(G + gr * p.sdo[2] + 8 * scc * p.sdo[3], p.sdo[3], vec_do));
+          put_raw(2 + x, load_raw8(O + gr * p.so[2] + 8 * scc * p.so[3], p.so[3], vec_o));
         } else {
           put_raw(x, zero_raw8<IO>());
           put_raw(2 + x, zero_raw8<IO>());
@@ -207,11 +212,11 @@ bwd_fused_kernel(const BwdParams p) {
       const int c0 = 32 * s + 8 * lg;
       float x[8], y[8];
       if (row < N) {
-        load8(K + row * p.sk[2] + c0 * p.sk[3], p.sk[3], p.vec_k, x);
+        load8(K + row * p.sk[2] + c0 * p.sk[3], p.sk[3], vec_k, x);
         float cs[8];
         rope_load4(tab, row + shift, D2, c0 / 2, cs);
         rope_rotate8(x, cs);
-        load8(V + row * p.sv[2] + c0 * p.sv[3], p.sv[3], p.vec_v, y);
+        load8(V + row * p.sv[2] + c0 * p.sv[3], p.sv[3], vec_v, y);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = y[e] = 0.f;
@@ -231,7 +236,7 @@ bwd_fused_kernel(const BwdParams p) {
       float x0[8], x1[8], cs0[8], cs1[8];
       const int r0 = 2 * rp, r1 = 2 * rp + 1;
       if (r0 < N) {
-        load8(K + r0 * p.sk[2] + 8 * cc * p.sk[3], p.sk[3], p.vec_k, x0);
+        load8(K + r0 * p.sk[2] + 8 * cc * p.sk[3], p.sk[3], vec_k, x0);
         rope_load4(tab, r0 + shift, D2, 4 * cc, cs0);
         rope_rotate8(x0, cs0);
       } else {
@@ -239,7 +244,7 @@ bwd_fused_kernel(const BwdParams p) {
         for (int e = 0; e < 8; ++e) x0[e] = 0.f;
       }
       if (r1 < N) {
-        load8(K + r1 * p.sk[2] + 8 * cc * p.sk[3], p.sk[3], p.vec_k, x1);
+        load8(K + r1 * p.sk[2] + 8 * cc * p.sk[3], p.sk[3], vec_k, x1);
         rope_load4(tab, r1 + shift, D2, 4 * cc, cs1);
         rope_rotate8(x1, cs1);
       } else {
@@ -378,7 +383,7 @@ bwd_fused_kernel(const BwdParams p) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) g4[r] = acc[i][r] * p.scale;
           rope_unrotate4(g4, tab, row + shift, D2, 8 * d + 2 * lg);
-          store4(dQ + row * p.sdq[2] + (16 * d + 4 * lg) * p.sdq[3], p.sdq[3], p.vec_dq, g4);
+          store4(dQ + row * p.sdq[2] + (16 * d + 4 * lg) * p.sdq[3], p.sdq[3], vec_dq, g4);
         }
       }
     }
@@ -394,9 +399,9 @@ bwd_fused_kernel(const BwdParams p) {
         float v4[4], g4[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) { v4[r] = dvacc[u][d][r]; g4[r] = dkacc[u][d][r] * p.scale; }
-        store4(dV + row * p.sdv[2] + (16 * d + 4 * lg) * p.sdv[3], p.sdv[3], p.vec_dv, v4);
+        store4(dV + row * p.sdv[2] + (16 * d + 4 * lg) * p.sdv[3], p.sdv[3], vec_dv, v4);
         rope_unrotate4(g4, tab, row + shift, D2, 8 * d + 2 * lg);
-        store4(dK + row * p.sdk[2] + (16 * d + 4 * lg) * p.sdk[3], p.sdk[3], p.vec_dk, g4);
+        store4(dK + row * p.sdk[2] + (16 * d + 4 * lg) * p.sdk[3], p.sdk[3], vec_dk, g4);
       }
     }
   }
@@ -409,8 +414,11 @@ int bwd_fused_rows() { return kFusedNW * kFusedKT * 16; }
 
 template <typename IO, int CT>
 static hipError_t fused_launch(const BwdParams& p, hipStream_t st) {
-  hipLaunchKernelGGL((bwd_fused_kernel<IO, CT, 64, kFusedNW, kFusedKT, kFusedQS>),
-                     dim3(p.B * p.H), dim3(kFusedNW * 64), 0, st, p);
+  const bool vec = p.vec_q && p.vec_k && p.vec_v && p.vec_o && p.vec_do && p.vec_dq && p.vec_dk &&
+                   p.vec_dv;
+  auto kern = vec ? bwd_fused_kernel<IO, CT, 64, kFusedNW, kFusedKT, kFusedQS, true>
+                  : bwd_fused_kernel<IO, CT, 64, kFusedNW, kFusedKT, kFusedQS, false>;
+  hipLaunchKernelGGL(kern, dim3(p.B * p.H), dim3(kFusedNW * 64), 0, st, p);
   return hipGetLastError();
 }
 

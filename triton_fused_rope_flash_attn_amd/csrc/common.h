@@ -286,17 +286,29 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 
 // Sum / max over the 4 lane groups that share one MFMA column (lanes
-// lr, lr+16, lr+32, lr+48).
-__device__ __forceinline__ float group4_sum(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+// lr, lr+16, lr+32, lr+48), with the gfx950 row-swap instructions (VALU, no
+// LDS round trip).  v_permlane16_swap(x, x) returns {x', x''} where, for
+// every lane, one of the two is the lane's own x and the other the x of
+// lane ^ 16; v_permlane32_swap does the same for lane ^ 32.  A commutative
+// op over the pair therefore combines each lane with its partner.
+__device__ __forceinline__ float xor16_pair_op_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
-__device__ __forceinline__ float group4_max(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
+__device__ __forceinline__ float xor32_pair_op_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
+__device__ __forceinline__ float xor16_pair_op_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_pair_op_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float group4_sum(float v) { return xor32_pair_op_sum(xor16_pair_op_sum(v)); }
+__device__ __forceinline__ float group4_max(float v) { return xor32_pair_op_max(xor16_pair_op_max(v)); }
 
 // Workgroups are dispatched round-robin over MI355X's 8 XCDs (each with its
 // own L2).  Remap the linear workgroup id so that XCD x processes one

@@ -7,29 +7,30 @@
 // for the backward pass (FA:308-309).
 //
 // gfx950 design:
-//  * A workgroup (NW waves) sweeps NW*QT q-subtiles of 16 rows of one (b, h)
-//    plane per pass; wave w takes subtiles w, w+NW, ... of the pass, so the
+//  * Persistent workgroups.  A work item is (b, h) plane x block of
+//    NW*QT*16 query rows (one item per plane when N <= 256 at D = 64).  Each
+//    workgroup walks its items with ONE continuous software pipeline: the next
+//    KV chunk -- of this item, or the first chunk of the next item -- is in
+//    flight in registers while the current chunk is computed, and the next
+//    item's Q rows are loaded while the current item runs.  HBM latency is
+//    therefore hidden behind compute even at one workgroup per CU.
+//  * Wave w owns q-subtiles w, w+NW, ... (16 rows each) of the item, so the
 //    ragged tail (N = 1 + H_img^2) is spread over the waves.  Rotated Q rows
-//    stay in registers as MFMA B-operands during a pass.  For N <= 256 one
-//    workgroup owns the whole plane and makes ceil(N/16 / (NW*QT)) passes
-//    over the K-hat/V^T it keeps in LDS, so K and V are staged once.
-//  * K and V are consumed in chunks of KC rows through a ring of NBUF LDS
-//    slots.  Chunk c+1 is loaded from HBM into registers while chunk c is
-//    being computed (one barrier per chunk); for N <= 256 the ring holds
-//    the whole plane.  K is rotated once per workgroup on its way into LDS
-//    (row-major K-hat, rows permuted so that the 16 rows one MFMA reads are
-//    consecutive: no bank conflicts); V is stored transposed (V^T), two keys
-//    per 32-bit LDS write.
+//    stay in registers as MFMA B-operands.
+//  * K and V go through a 2-slot LDS ring of KC-key chunks.  K is rotated in
+//    fp32 on its way in (row-major K-hat, rows permuted so the 16 rows one
+//    MFMA reads are consecutive: no bank conflicts); V is stored transposed,
+//    two keys per 32-bit LDS write.  The ragged chunk of a plane is processed
+//    first, so the cross-item prefetch always overlaps a full chunk.
 //  * Logits are computed transposed, S^T = K-hat Q-hat^T, with key
 //    kv = 8*(r/4) + 4*h + r%4 of a 32-key block in A-row r of half h.  Lane
 //    group lg then holds keys 8*lg .. 8*lg+7 of its query column: exactly the
-//    B-operand of O^T += V^T P^T, so P never leaves registers and each V^T
-//    fragment is one 16-byte LDS read shared by all QT subtiles.
+//    B-operand of O^T += V^T P^T, so P never leaves registers and each K-hat /
+//    V^T fragment (one 16-byte LDS read) feeds all QT subtiles of the wave.
 //  * One query row per lane: the row max needs two cross-lane steps per
 //    32-key block.  Softmax runs in base 2 (log2(e) folded into the scale)
 //    with fp32 state and accumulator; O and the row sum are rescaled only
-//    when the running max grows by more than 2^8 (P <= 256 otherwise), so
-//    the rescale is rare after the first block.
+//    when the running max grows by more than 2^8 (P <= 256 otherwise).
 #include <type_traits>
 
 #include "common.h"
@@ -66,10 +67,20 @@ __device__ __forceinline__ int kperm(int r) {
   return (r & ~31) | ((r & 4) << 2) | ((r & 24) >> 1) | (r & 3);
 }
 
+// V^T tile: the 8-key group g of channel row d is stored at group
+// g ^ ((d >> 3) & 7).  With a row pitch of KC + 16 elements this makes both
+// the transposed stores (8 channel rows x 2 key pairs per 16 lanes) and the
+// MFMA fragment reads (16 channel rows, one group) bank-conflict free.
+__device__ __forceinline__ int vswz(int d, int col) {
+  return (((col >> 3) ^ ((d >> 3) & 7)) << 3) | (col & 7);
+}
+
 constexpr float kRescaleSlack = 8.0f;   // log2 units: P <= 2^8 between rescales
 
-template <typename IO, int CT, int D, int NW, int QT, int KC, int NBUF>
-__global__ void __launch_bounds__(NW * 64, 2)
+// VEC: every tensor of the call allows 16-byte vector access (decided on the
+// host); the generic instantiation gathers element by element instead.
+template <typename IO, int CT, int D, int NW, int QT, int KC, int TABROWS, bool VEC>
+__global__ void __launch_bounds__(NW * 64)
 fwd_kernel(const FwdParams p) {
   using C = Comp<CT>;
   using S = typename C::S;
@@ -79,39 +90,75 @@ fwd_kernel(const FwdParams p) {
   constexpr int D2 = D / 2;
   constexpr int PADE = 16 / sizeof(S);
   constexpr int LDK = D + PADE;       // K-hat row pitch (elements)
-  constexpr int LDV = KC + PADE;      // V^T row pitch
+  constexpr int LDV = KC + 16;        // V^T row pitch (elements; see vswz)
   constexpr int NT = NW * 64;
   constexpr int CPR = D / 8;          // 8-channel chunks per row
   constexpr int UNITS = (KC / 2) * CPR;   // (row pair, chunk) staging units per KV chunk
   constexpr int ITER = (UNITS + NT - 1) / NT;
-  constexpr bool kPlane = NBUF * KC >= 256;   // LDS ring holds a whole plane (host: N <= 256)
   static_assert(KC % 32 == 0, "KV chunk must be a multiple of 32 keys");
+  // TABROWS > 0: the whole packed RoPE table (<= TABROWS rows) is copied into
+  // LDS once per persistent workgroup and all rotations read it from there;
+  // TABROWS == 0: rotations read the table from global memory (L2-resident).
+  constexpr bool kTabLds = TABROWS > 0;
 
-  __shared__ __attribute__((aligned(16))) S sK[NBUF][KC * LDK];
-  __shared__ __attribute__((aligned(16))) S sVt[NBUF][D * LDV];
+  __shared__ __attribute__((aligned(16))) S sK[2][KC * LDK];
+  __shared__ __attribute__((aligned(16))) S sVt[2][D * LDV];
+  // LDS copy of the packed table: row pitch D + 4 floats (bank-spread rows).
+  constexpr int TP = D + 4;
+  __shared__ __attribute__((aligned(16))) float sTab[kTabLds ? TABROWS * TP : 4];
 
   const int N = p.N;
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
-  const int plane = tile / p.n_blk;
-  const int qblk = tile - plane * p.n_blk;
-  const int bb = plane / p.H, hh = plane - bb * p.H;
-  const IO* __restrict__ Q = static_cast<const IO*>(p.q) + bb * p.sq[0] + hh * p.sq[1];
-  const IO* __restrict__ K = static_cast<const IO*>(p.k) + bb * p.sk[0] + hh * p.sk[1];
-  const IO* __restrict__ V = static_cast<const IO*>(p.v) + bb * p.sv[0] + hh * p.sv[1];
-  IO* __restrict__ O = static_cast<IO*>(p.o) + bb * p.so[0] + hh * p.so[1];
-  const float* __restrict__ tab = p.rope;
+  const int nch = (N + KC - 1) / KC;  // KV chunks per item
+  const bool vec_q = VEC || p.vec_q, vec_k = VEC || p.vec_k;
+  const bool vec_v = VEC || p.vec_v, vec_o = VEC || p.vec_o;
   const int shift = 1 - p.has_cls;    // table row of token s is s + shift
-  const bool vec_k = p.vec_k, vec_v = p.vec_v;
+  const float c2 = p.scale_log2;
+  // cos/sin of pairs p0 .. p0+3 of table row `row`.  `swap` lanes fetch the
+  // two 16-byte halves in the opposite order (spreads banks when neighbouring
+  // lanes read the same columns of two rows).
+  auto tab4 = [&](int row, int p0, float (&cs)[8], int swap) {
+    if constexpr (kTabLds) {
+      const f32x4* t = reinterpret_cast<const f32x4*>(&sTab[row * TP + 2 * p0]);
+      const f32x4 a = t[swap], b = t[swap ^ 1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        cs[e] = swap ? b[e] : a[e];
+        cs[4 + e] = swap ? a[e] : b[e];
+      }
+    } else {
+      rope_load4(p.rope, row, D2, p0, cs);
+    }
+  };
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (SGPR)
   const int lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
 
-  // ---- KV chunk prefetch registers: two rows x 8 channels of K, V, (cos, sin) ----
+  // Item of this workgroup at iteration `it` (-1 when done).  Within an
+  // iteration, items are dealt XCD-major so neighbouring items (the q blocks
+  // of one plane) run on the same XCD and share its L2.
+  const int pos = xcd_remap(blockIdx.x, gridDim.x);
+  auto item_of = [&](int it) {
+    const int item = it * (int)gridDim.x + pos;
+    return item < p.n_items ? item : -1;
+  };
+  auto plane_base = [&](const void* base, const int64_t* st, int plane) {
+    const int bb = plane / p.H, hh = plane - bb * p.H;
+    return static_cast<const IO*>(base) + bb * st[0] + hh * st[1];
+  };
+  // Chunk c of an item starts at key ((c + nch - 1) % nch) * KC: ragged chunk first.
+  auto chunk_start = [&](int c) { return ((c + nch - 1) % nch) * KC; };
+
+  // ---- KV chunk prefetch registers: two rows x 8 channels of K and V
+  //      (+ their cos/sin when the table is not in LDS) ----
   Raw8<IO> pk[ITER][2], pv[ITER][2];
-  float pcs[ITER][2][8];
-  auto prefetch = [&](int kvb) {
+  float pcs[ITER][2][kTabLds ? 1 : 8];
+  auto prefetch_kv = [&](int item, int c) {
+    const int plane = item / p.n_blk;
+    const IO* __restrict__ K = plane_base(p.k, p.sk, plane);
+    const IO* __restrict__ V = plane_base(p.v, p.sv, plane);
+    const int kvb = chunk_start(c);
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
       const int u = tid + it * NT;
@@ -122,17 +169,19 @@ fwd_kernel(const FwdParams p) {
         if (u < UNITS && gr < N) {
           pk[it][x] = load_raw8(K + gr * p.sk[2] + 8 * cc * p.sk[3], p.sk[3], vec_k);
           pv[it][x] = load_raw8(V + gr * p.sv[2] + 8 * cc * p.sv[3], p.sv[3], vec_v);
-          rope_load4(tab, gr + shift, D2, 4 * cc, pcs[it][x]);
+          if constexpr (!kTabLds) rope_load4(p.rope, gr + shift, D2, 4 * cc, pcs[it][x]);
         } else {
           pk[it][x] = zero_raw8<IO>();
           pv[it][x] = zero_raw8<IO>();
+          if constexpr (!kTabLds) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) pcs[it][x][e] = 0.f;
+            for (int e = 0; e < 8; ++e) pcs[it][x][e] = 0.f;
+          }
         }
       }
     }
   };
-  auto commit = [&](int slot) {
+  auto commit_kv = [&](int slot, int kvb) {
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
       const int u = tid + it * NT;
@@ -143,135 +192,196 @@ fwd_kernel(const FwdParams p) {
         for (int x = 0; x < 2; ++x) {
           float xk[8];
           unpack8(pk[it][x], xk);
-          rope_rotate8(xk, pcs[it][x]);
+          if constexpr (kTabLds) {
+            // rows past N hold zeros; any in-table row serves for them
+            float cs[8];
+            tab4(min(kvb + 2 * rp + x, N - 1) + shift, 4 * cc, cs, rp & 1);
+            rope_rotate8(xk, cs);
+          } else {
+            rope_rotate8(xk, pcs[it][x]);
+          }
           C::put8(&sK[slot][kperm(2 * rp + x) * LDK + 8 * cc], xk);
           unpack8(pv[it][x], xv[x]);
         }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) put2<CT>(&sVt[slot][(8 * cc + e) * LDV + 2 * rp], xv[0][e], xv[1][e]);
+        for (int e = 0; e < 8; ++e)
+          put2<CT>(&sVt[slot][(8 * cc + e) * LDV + vswz(8 * cc + e, 2 * rp)], xv[0][e], xv[1][e]);
       }
     }
   };
 
-  Frag qf[QT][KS];
-  float m_run[QT], l_run[QT];
-  f32x4 oacc[QT][DT];
-  const float c2 = p.scale_log2;
-  const int nsub = (N + 15) / 16;            // 16-row q-subtiles of the plane
-  // Pass `ps` of this workgroup covers subtiles base + t*NW + wave, t < QT.
-  auto pass_base = [&](int ps) { return (qblk + ps) * NW * QT; };
-
-  // ---- rotated Q rows of one pass -> B-operand fragments; returns the number
-  //      of active subtiles of this wave (a prefix t < nt, wave-uniform) ----
-  auto load_q = [&](int ps) {
-    int nt = 0;
+  // ---- Q rows of an item: raw prefetch registers -> rotated B-operand fragments ----
+  Raw8<IO> qraw[QT][KS];
+  float qcs[QT][KS][kTabLds ? 1 : 8];
+  auto prefetch_q = [&](int item) {
+    const int plane = item / p.n_blk, qb = item - plane * p.n_blk;
+    const IO* __restrict__ Q = plane_base(p.q, p.sq, plane);
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
-      const int sub = pass_base(ps) + t * NW + wave;
-      nt += sub < nsub;
-      const int row = sub * 16 + lr;
+      const int row = (qb * NW * QT + t * NW + wave) * 16 + lr;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const int c0 = 32 * s + 8 * lg;
+        if (row < N) {
+          qraw[t][s] = load_raw8(Q + row * p.sq[2] + c0 * p.sq[3], p.sq[3], vec_q);
+          if constexpr (!kTabLds) rope_load4(p.rope, row + shift, D2, c0 / 2, qcs[t][s]);
+        } else {
+          qraw[t][s] = zero_raw8<IO>();
+          if constexpr (!kTabLds) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qcs[t][s][e] = 0.f;
+          }
+        }
+      }
+    }
+  };
+  Frag qf[QT][KS];
+  auto commit_q = [&](int qb) {
+#pragma unroll
+    for (int t = 0; t < QT; ++t)
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         float x[8];
-        const int c0 = 32 * s + 8 * lg;
-        if (row < N) {
-          load8(Q + row * p.sq[2] + c0 * p.sq[3], p.sq[3], p.vec_q, x);
+        unpack8(qraw[t][s], x);
+        if constexpr (kTabLds) {
+          const int row = (qb * NW * QT + t * NW + wave) * 16 + lr;
           float cs[8];
-          rope_load4(tab, row + shift, D2, c0 / 2, cs);
+          tab4(min(row, N - 1) + shift, 16 * s + 4 * lg, cs, 0);
           rope_rotate8(x, cs);
         } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] = 0.f;
+          rope_rotate8(x, qcs[t][s]);
         }
         qf[t][s] = C::make(x);
       }
+  };
+
+  float m_run[QT], l_run[QT];
+  f32x4 oacc[QT][DT];
+
+  // One KV chunk for all QT subtiles of the wave.  Subtiles past the last
+  // query row hold zero rows and are computed anyway: every wave of a
+  // workgroup then runs the same instruction stream with no per-subtile
+  // guards, and for the 16-row-ragged N of ViT planes the extra work lands on
+  // SIMDs that would otherwise wait at the next barrier.
+  // One 32-key block for all QT subtiles of the wave.  Subtiles past the last
+  // query row hold zero rows and are computed anyway: every wave of a
+  // workgroup then runs the same instruction stream with no per-subtile
+  // guards, and for the 16-row-ragged N of ViT planes the extra work lands on
+  // SIMDs that would otherwise wait at the next barrier.  MASKED: the block
+  // holding key N-1 (keys >= N get probability 0).
+  auto block = [&](auto maskc, const S* __restrict__ cK, const S* __restrict__ cV, int kvb, int j) {
+    constexpr bool MASKED = decltype(maskc)::value;
+    // ---- S^T = K-hat Q-hat^T for 32 keys (each K-hat fragment feeds QT MFMAs) ----
+    f32x4 sacc[QT][2];
+#pragma unroll
+    for (int t = 0; t < QT; ++t) sacc[t][0] = sacc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const Frag a = C::lds(&cK[(32 * j + 16 * h + lr) * LDK + 32 * s + 8 * lg]);
+#pragma unroll
+        for (int t = 0; t < QT; ++t) sacc[t][h] = C::mma(a, qf[t][s], sacc[t][h]);
+      }
+    }
+    // ---- online softmax; lane holds keys kvb + 32j + 8lg + (0..7) of its row ----
+    const int lim = N - (kvb + 32 * j + 8 * lg);   // keys e < lim are valid (MASKED only)
+    Frag pf[QT];
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+      float sv[8];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[4 * h + i] = sacc[t][h][i];
+      if constexpr (MASKED) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sv[e] = e < lim ? sv[e] : -INFINITY;
+      }
+      float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                       fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+      mx = group4_max(mx) * c2;
+      if (__any(mx > m_run[t] + kRescaleSlack)) {
+        const float mnew = fmaxf(m_run[t], mx);
+        const float alpha = fast_exp2(m_run[t] - mnew);
+        l_run[t] *= alpha;
+#pragma unroll
+        for (int d = 0; d < DT; ++d) oacc[t][d] *= alpha;
+        m_run[t] = mnew;
+      }
+      float pv8[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pv8[e] = fast_exp2(__builtin_fmaf(sv[e], c2, -m_run[t]));
+        l_run[t] += pv8[e];
+      }
+      pf[t] = C::make(pv8);
+    }
+    // ---- O^T += V^T P^T (each V^T fragment feeds QT MFMAs) ----
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+      const Frag a = C::lds(&cV[(16 * d + lr) * LDV + vswz(16 * d + lr, 32 * j + 8 * lg)]);
+#pragma unroll
+      for (int t = 0; t < QT; ++t) oacc[t][d] = C::mma(a, pf[t], oacc[t][d]);
+    }
+  };
+  // One KV chunk: full blocks, then the block holding key N-1 if it is ragged.
+  auto chunk = [&](const S* __restrict__ cK, const S* __restrict__ cV, int kvb) {
+    const int nkeys = min(KC, N - kvb);
+    const int nfull = nkeys / 32;
+    for (int j = 0; j < nfull; ++j) block(std::false_type{}, cK, cV, kvb, j);
+    if (nkeys % 32) block(std::true_type{}, cK, cV, kvb, nfull);
+  };
+
+  int it = 0;
+  int item = item_of(0);
+  if (item < 0) return;
+  prefetch_kv(item, 0);
+  prefetch_q(item);
+  if constexpr (kTabLds) {
+    // rows 0 .. N-1+shift of the packed table, D floats each -> pitch TP
+    constexpr int V4 = D / 4;   // f32x4 per row
+    const f32x4* src = reinterpret_cast<const f32x4*>(p.rope);
+    for (int i = tid; i < (N + shift) * V4; i += NT) {
+      const int r = i / V4, c = i - r * V4;
+      *reinterpret_cast<f32x4*>(&sTab[r * TP + 4 * c]) = src[i];
+    }
+    __syncthreads();
+  }
+  int g = 0;   // chunks consumed so far: LDS slot g & 1
+  while (item >= 0) {
+    const int plane = item / p.n_blk, qb = item - plane * p.n_blk;
+    const int nxt = item_of(it + 1);
+    commit_q(qb);
+    int nt = 0;   // active subtiles of this wave: a prefix t < nt (wave-uniform)
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+      nt += (qb * NW * QT + t * NW + wave) * 16 < N;
       m_run[t] = -INFINITY;
       l_run[t] = 0.f;
 #pragma unroll
       for (int d = 0; d < DT; ++d) oacc[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    return nt;
-  };
 
-  // One KV chunk for the first NTA subtiles (NTA is a compile-time count so
-  // the MFMA / softmax stream carries no per-subtile guards).
-  auto chunk = [&](auto ntc, const S* __restrict__ cK, const S* __restrict__ cV, int kvb) {
-    constexpr int NTA = decltype(ntc)::value;
-    const int nblk = min(KC, round_up32(N - kvb)) / 32;
-    for (int j = 0; j < nblk; ++j) {
-      // ---- S^T = K-hat Q-hat^T for 32 keys (each K-hat fragment feeds NTA MFMAs) ----
-      f32x4 sacc[NTA][2];
-#pragma unroll
-      for (int t = 0; t < NTA; ++t) sacc[t][0] = sacc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const Frag a = C::lds(&cK[(32 * j + 16 * h + lr) * LDK + 32 * s + 8 * lg]);
-#pragma unroll
-          for (int t = 0; t < NTA; ++t) sacc[t][h] = C::mma(a, qf[t][s], sacc[t][h]);
-        }
+    for (int c = 0; c < nch; ++c, ++g) {
+      const int slot = g & 1;
+      commit_kv(slot, chunk_start(c));
+      if (c + 1 < nch) {
+        prefetch_kv(item, c + 1);
+      } else if (nxt >= 0) {
+        prefetch_kv(nxt, 0);
       }
-      // ---- online softmax; lane holds keys kvb + 32j + 8lg + (0..7) of its row ----
-      const int kbase = kvb + 32 * j + 8 * lg;
-      const bool masked = kvb + 32 * j + 32 > N;
-      Frag pf[NTA];
-#pragma unroll
-      for (int t = 0; t < NTA; ++t) {
-        float sv[8];
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) sv[4 * h + i] = sacc[t][h][i];
-        if (masked) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) sv[e] = kbase + e < N ? sv[e] : -INFINITY;
-        }
-        float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                         fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-        mx = group4_max(mx) * c2;
-        if (__any(mx > m_run[t] + kRescaleSlack)) {
-          const float mnew = fmaxf(m_run[t], mx);
-          const float alpha = fast_exp2(m_run[t] - mnew);
-          l_run[t] *= alpha;
-#pragma unroll
-          for (int d = 0; d < DT; ++d) oacc[t][d] *= alpha;
-          m_run[t] = mnew;
-        }
-        float pv8[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          pv8[e] = fast_exp2(__builtin_fmaf(sv[e], c2, -m_run[t]));
-          l_run[t] += pv8[e];
-        }
-        pf[t] = C::make(pv8);
-      }
-      // ---- O^T += V^T P^T (each V^T fragment feeds NTA MFMAs) ----
-#pragma unroll
-      for (int d = 0; d < DT; ++d) {
-        const Frag a = C::lds(&cV[(16 * d + lr) * LDV + 32 * j + 8 * lg]);
-#pragma unroll
-        for (int t = 0; t < NTA; ++t) oacc[t][d] = C::mma(a, pf[t], oacc[t][d]);
-      }
+      if (c == 0 && nxt >= 0) prefetch_q(nxt);
+      __syncthreads();
+      if (nt > 0) chunk(sK[slot], sVt[slot], chunk_start(c));
     }
-  };
-  auto run_chunk = [&](int nt, int slot, int kvb) {
-    if (nt == QT) {
-      chunk(std::integral_constant<int, QT>{}, sK[slot], sVt[slot], kvb);
-    } else if (nt > 0) {
-      if constexpr (QT >= 3) {
-        if (nt == 2) { chunk(std::integral_constant<int, 2>{}, sK[slot], sVt[slot], kvb); return; }
-      }
-      chunk(std::integral_constant<int, 1>{}, sK[slot], sVt[slot], kvb);
-    }
-  };
 
-  // ---- epilogue of a pass: lane holds O[row][16d + 4lg + (0..3)] ----
-  auto store_pass = [&](int ps, int nt) {
+    // ---- epilogue: lane holds O[row][16d + 4lg + (0..3)] ----
+    IO* __restrict__ O = const_cast<IO*>(plane_base(p.o, p.so, plane));
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
       const float l = group4_sum(l_run[t]);
-      const int row = (pass_base(ps) + t * NW + wave) * 16 + lr;
+      const int row = (qb * NW * QT + t * NW + wave) * 16 + lr;
       if (t < nt && row < N) {
         const float inv = 1.f / l;
 #pragma unroll
@@ -279,93 +389,67 @@ fwd_kernel(const FwdParams p) {
           float o4[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) o4[r] = oacc[t][d][r] * inv;
-          store4(O + row * p.so[2] + (16 * d + 4 * lg) * p.so[3], p.so[3], p.vec_o, o4);
+          store4(O + row * p.so[2] + (16 * d + 4 * lg) * p.so[3], p.so[3], vec_o, o4);
         }
         if (lg == 0) p.lse[(int64_t)plane * N + row] = (m_run[t] + fast_log2(l)) * kLn2;
       }
     }
-  };
-
-  prefetch(0);
-  int nt = load_q(0);
-
-  // ---- pass 0: software-pipelined over KV chunks ----
-  const int nchunks = (N + KC - 1) / KC;
-  for (int c = 0; c < nchunks; ++c) {
-    const int slot = c % NBUF;
-    const int kvb = c * KC;
-    commit(slot);
-    if (c + 1 < nchunks) prefetch(kvb + KC);
-    __syncthreads();
-    run_chunk(nt, slot, kvb);
-  }
-  store_pass(0, nt);
-
-  // ---- further passes (plane-resident variant: every chunk is still in LDS) ----
-  if constexpr (kPlane) {
-    const int npass = (nsub - pass_base(0) + NW * QT - 1) / (NW * QT);
-    for (int ps = 1; ps < npass; ++ps) {
-      nt = load_q(ps);
-      for (int c = 0; c < nchunks; ++c) run_chunk(nt, c, c * KC);
-      store_pass(ps, nt);
-    }
+    item = nxt;
+    ++it;
   }
 }
 
 // ---------------------------------------------------------------------------
-// Tile table for the forward pass: (NW, QT, KC, NBUF) per head_dim/variant.
+// Tile table for the forward pass: (NW, QT, KC) per head_dim.  One work item
+// covers NW*QT*16 query rows of a plane; workgroups are persistent.
 // ---------------------------------------------------------------------------
-template <int D, int VAR> struct FwdShape;
-// plane-resident: 4 slots x 64 keys = 256 keys in LDS; 4 waves x 2 subtiles
-// = 128 query rows per pass, ceil(N/128) passes over the resident K-hat/V^T.
-template <> struct FwdShape<64, FWD_PLANE> { static constexpr int NW = 4, QT = 2, KC = 64, NBUF = 4; };
-template <> struct FwdShape<64, FWD_STREAM> { static constexpr int NW = 4, QT = 2, KC = 64, NBUF = 2; };
-template <> struct FwdShape<128, FWD_STREAM> { static constexpr int NW = 4, QT = 1, KC = 32, NBUF = 2; };
+// TABROWS: rows of the packed RoPE table an LDS-resident copy can hold
+// (N + 1 - has_cls <= TABROWS; i.e. planes up to 256 tokens).
+template <int D> struct FwdShape;
+template <> struct FwdShape<64> { static constexpr int NW = 8, QT = 2, KC = 128, TABROWS = 257; };
+template <> struct FwdShape<128> { static constexpr int NW = 8, QT = 1, KC = 64, TABROWS = 0; };
 
-int fwd_block_rows(int D, int variant) {
-  if (D == 64 && variant == FWD_PLANE) {
-    using SH = FwdShape<64, FWD_PLANE>;
-    return SH::NBUF * SH::KC;   // one workgroup per plane
-  }
-  if (D == 64) {
-    using SH = FwdShape<64, FWD_STREAM>;
-    return SH::NW * SH::QT * 16;
-  }
-  using SH = FwdShape<128, FWD_STREAM>;
-  return SH::NW * SH::QT * 16;
+int fwd_block_rows(int D) {
+  return D == 64 ? FwdShape<64>::NW * FwdShape<64>::QT * 16 : FwdShape<128>::NW * FwdShape<128>::QT * 16;
 }
+int fwd_threads(int D) { return D == 64 ? FwdShape<64>::NW * 64 : FwdShape<128>::NW * 64; }
 
-template <typename IO, int CT, int D, int VAR>
+template <typename IO, int CT, int D>
 static hipError_t fwd_launch(const FwdParams& p, hipStream_t st) {
-  using SH = FwdShape<D, VAR>;
-  const int grid = p.B * p.H * p.n_blk;
-  hipLaunchKernelGGL((fwd_kernel<IO, CT, D, SH::NW, SH::QT, SH::KC, SH::NBUF>), dim3(grid),
-                     dim3(SH::NW * 64), 0, st, p);
+  using SH = FwdShape<D>;
+  // fp32 compute keeps 4-byte tiles in LDS: no room for the table copy there
+  constexpr int TR = CT == DT_F32 ? 0 : SH::TABROWS;
+  const bool tab = TR > 0 && p.N + 1 - p.has_cls <= TR;
+  const bool vec = p.vec_q && p.vec_k && p.vec_v && p.vec_o;
+  auto kern = tab ? (vec ? fwd_kernel<IO, CT, D, SH::NW, SH::QT, SH::KC, TR, true>
+                         : fwd_kernel<IO, CT, D, SH::NW, SH::QT, SH::KC, TR, false>)
+                  : (vec ? fwd_kernel<IO, CT, D, SH::NW, SH::QT, SH::KC, 0, true>
+                         : fwd_kernel<IO, CT, D, SH::NW, SH::QT, SH::KC, 0, false>);
+  const int grid = persistent_grid(reinterpret_cast<const void*>(kern), SH::NW * 64, p.n_items);
+  if (grid <= 0) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(SH::NW * 64), 0, st, p);
   return hipGetLastError();
 }
 
 template <typename IO, int CT>
-static hipError_t fwd_shape(const FwdParams& p, int D, int variant, hipStream_t st) {
-  if (D == 64)
-    return variant == FWD_PLANE ? fwd_launch<IO, CT, 64, FWD_PLANE>(p, st)
-                                : fwd_launch<IO, CT, 64, FWD_STREAM>(p, st);
-  return fwd_launch<IO, CT, 128, FWD_STREAM>(p, st);
+static hipError_t fwd_shape(const FwdParams& p, int D, hipStream_t st) {
+  return D == 64 ? fwd_launch<IO, CT, 64>(p, st) : fwd_launch<IO, CT, 128>(p, st);
 }
 
 template <typename IO>
-static hipError_t fwd_ct(const FwdParams& p, int ct, int D, int variant, hipStream_t st) {
+static hipError_t fwd_ct(const FwdParams& p, int ct, int D, hipStream_t st) {
   switch (ct) {
-    case DT_BF16: return fwd_shape<IO, DT_BF16>(p, D, variant, st);
-    case DT_F16: return fwd_shape<IO, DT_F16>(p, D, variant, st);
-    default: return fwd_shape<IO, DT_F32>(p, D, variant, st);
+    case DT_BF16: return fwd_shape<IO, DT_BF16>(p, D, st);
+    case DT_F16: return fwd_shape<IO, DT_F16>(p, D, st);
+    default: return fwd_shape<IO, DT_F32>(p, D, st);
   }
 }
 
-hipError_t launch_fwd(const FwdParams& p, int io, int ct, int D, int variant, hipStream_t st) {
+hipError_t launch_fwd(const FwdParams& p, int io, int ct, int D, hipStream_t st) {
   switch (io) {
-    case DT_BF16: return fwd_ct<bf16>(p, ct, D, variant, st);
-    case DT_F16: return fwd_ct<f16>(p, ct, D, variant, st);
-    default: return fwd_ct<float>(p, ct, D, variant, st);
+    case DT_BF16: return fwd_ct<bf16>(p, ct, D, st);
+    case DT_F16: return fwd_ct<f16>(p, ct, D, st);
+    default: return fwd_ct<float>(p, ct, D, st);
   }
 }
 

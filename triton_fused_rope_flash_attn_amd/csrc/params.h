@@ -21,6 +21,7 @@ struct FwdParams {
   float scale_log2;    // softmax_scale * log2(e)
   int vec_q, vec_k, vec_v, vec_o;
   int n_blk;           // q blocks per plane
+  int n_items;         // planes * n_blk work items
 };
 
 struct BwdParams {
@@ -44,17 +45,13 @@ struct BwdParams {
 };
 
 // Launch shapes picked by the tile table (api.hip).
-enum FwdVariant : int {
-  FWD_PLANE = 0,    // one workgroup per (b,h) plane, K-hat/V^T of the plane kept in LDS (N <= 256)
-  FWD_STREAM = 1,   // kv chunks streamed through a double-buffered LDS ring (any N)
-};
 enum BwdVariant : int {
   BWD_FUSED = 0,    // one workgroup per plane: dK, dV and dQ in one pass (N <= 256)
   BWD_SPLIT = 1,    // dQ kernel (Q-outer, also writes delta) + dK/dV kernel (KV-outer)
 };
 
 // Launchers: return hipSuccess or the launch error.  io/ct are DT_* codes.
-hipError_t launch_fwd(const FwdParams& p, int io, int ct, int D, int variant, hipStream_t st);
+hipError_t launch_fwd(const FwdParams& p, int io, int ct, int D, hipStream_t st);
 hipError_t launch_bwd_pre(const BwdParams& p, int io, int D, hipStream_t st);
 hipError_t launch_bwd_dq(const BwdParams& p, int io, int ct, int D, bool write_delta,
                          hipStream_t st);
@@ -65,8 +62,12 @@ hipError_t launch_rope_pack(const float* cosp, int64_t cs0, int64_t cs1, const f
                             int64_t ss0, int64_t ss1, int n_pos, int d2, float* out,
                             hipStream_t st);
 
-// Rows of q (fwd, dq) or kv (dk/dv) one workgroup covers, per variant.
-int fwd_block_rows(int D, int variant);
+// Workgroups for a persistent kernel: min(items, CUs x resident workgroups per CU).
+int persistent_grid(const void* kernel, int block_threads, int items);
+
+// Rows of q (fwd, dq) or kv (dk/dv) one work item / workgroup covers.
+int fwd_block_rows(int D);
+int fwd_threads(int D);
 int bwd_dq_block_rows(int D);
 int bwd_dkdv_block_rows(int D);
 int bwd_fused_rows();
