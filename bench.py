@@ -72,28 +72,31 @@ def make_inputs(wl, device, seed=0, dtype=None):
     return [t.to(dtype).to(device) for t in ts]
 
 
-def time_cpu_baseline(wl, budget_s=10.0):
-    """Oracle fwd+bwd in fp32 on the host over B_slice batch rows of the workload."""
+def time_cpu_baseline(wl, budget_s=12.0):
+    """Oracle fwd+bwd in fp32 on the host over a slice of the workload's batch.
+
+    Runs whole fwd+bwd iterations until `budget_s` seconds of CPU work have
+    been timed (at least 3), with the thread count capped at the process's
+    share of the host (OMP_NUM_THREADS, else the affinity mask)."""
     import torch
     from oracle import torch_ref
     from triton_fused_rope_flash_attn_amd import build_axial_rope_pairs
 
     cores = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        cores = min(cores, int(os.environ["OMP_NUM_THREADS"]))
     torch.set_num_threads(cores)
     sub = dict(wl, B=4 if wl["D"] == 64 else 1)
     q, k, v, do = make_inputs(sub, "cpu", dtype=torch.float32)
     cosp, sinp = build_axial_rope_pairs(wl["side"], wl["D"], torch.device("cpu"), base=100.0)
     B, H, N, D = q.shape
     times = []
-    for i in range(3):
-        torch_ref.forward_backward(q, k, v, do, cosp, sinp, wl["has_cls"])
+    torch_ref.forward_backward(q, k, v, do, cosp, sinp, wl["has_cls"])  # warm-up
     t_start = time.perf_counter()
-    while True:
+    while len(times) < 3 or time.perf_counter() - t_start < budget_s:
         t0 = time.perf_counter()
         torch_ref.forward_backward(q, k, v, do, cosp, sinp, wl["has_cls"])
         times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > budget_s or len(times) >= 200:
-            break
     med = statistics.median(times)
     _, _, fall = flops(B, H, N, D)
     cpu_model = ""
@@ -113,7 +116,7 @@ def time_cpu_baseline(wl, budget_s=10.0):
         "sample": (
             f"oracle (Python 2D RoPE + torch SDPA math, fp32, autograd) fwd+bwd on B={B} of "
             f"{wl['B']} (planes {B * H} of {wl['B'] * H}), N={N}, D={D}; median of {len(times)} "
-            f"iterations, {med * 1e3:.1f} ms each; CPU: {cpu_model}"
+            f"iterations ({sum(times):.1f} s timed), {med * 1e3:.1f} ms each; {cores} threads; CPU: {cpu_model}"
         ),
     }
 
@@ -252,7 +255,7 @@ def main():
     desc = _lib.make_desc(B, H, N, D, n_pos, wl["has_cls"], _lib.BF16, _lib.BF16, scale)
     bwd_cfg = _lib.tile_config(desc, 1)
     fwd_cfg = _lib.tile_config(desc, 0)
-    bwd_kernel = "bwd_dkdv_kernel<FUSED>" if bwd_cfg[0] == 0 else "bwd_dq_kernel + bwd_dkdv_kernel"
+    bwd_kernel = "bwd_fused_kernel" if bwd_cfg[0] == 0 else "bwd_dq_kernel + bwd_dkdv_kernel"
 
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
