@@ -68,9 +68,12 @@ bwd_dq_kernel(const BwdParams p) {
   constexpr int NT = NW * 64, CPR = D / 8;
   constexpr int ITER = (KVS * CPR + NT - 1) / NT;
   constexpr int QROWS = NW * QT * 16;
+  // 16-bit operands: K-hat^T is read transposed from sK (ds_read_b64_tr_b16);
+  // fp32 storage keeps an explicit transposed copy.
+  constexpr bool TR = sizeof(S) == 2;
 
   __shared__ __attribute__((aligned(16))) S sK[KVS * LDK];
-  __shared__ __attribute__((aligned(16))) S sKt[D * LDT];
+  __shared__ __attribute__((aligned(16))) S sKt[TR ? 8 : D * LDT];
   __shared__ __attribute__((aligned(16))) S sV[KVS * LDK];
 
   const int N = p.N;
@@ -166,8 +169,10 @@ bwd_dq_kernel(const BwdParams p) {
           rope_rotate8(xk[it], cs[it]);
           C::put8(&sK[r * LDK + 8 * cc], xk[it]);
           C::put8(&sV[r * LDK + 8 * cc], xv[it]);
+          if constexpr (!TR) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) C::put1(&sKt[(8 * cc + e) * LDT + r], xk[it][e]);
+            for (int e = 0; e < 8; ++e) C::put1(&sKt[(8 * cc + e) * LDT + r], xk[it][e]);
+          }
         }
       }
     }
@@ -211,7 +216,13 @@ bwd_dq_kernel(const BwdParams p) {
       }
 #pragma unroll
       for (int d = 0; d < DT; ++d) {
-        const Frag a = C::lds(&sKt[(16 * d + lr) * LDT + 32 * j + 8 * lg]);
+        // A = K-hat^T rows 16d.., k-slot e <-> key 32j + 8lg + e (the dS^T order)
+        Frag a;
+        if constexpr (TR)
+          a = C::tr(&sK[tr_offset(32 * j + 8 * lg, 16 * d, LDK, lr)],
+                    &sK[tr_offset(32 * j + 8 * lg + 4, 16 * d, LDK, lr)]);
+        else
+          a = C::lds(&sKt[(16 * d + lr) * LDT + 32 * j + 8 * lg]);
 #pragma unroll
         for (int t = 0; t < QT; ++t) dqacc[t][d] = C::mma(a, dsf[t], dqacc[t][d]);
       }
@@ -249,11 +260,14 @@ bwd_dkdv_kernel(const BwdParams p) {
   constexpr int NT = NW * 64, CPR = D / 8;
   constexpr int ITER = (QS * CPR + NT - 1) / NT;
   constexpr int KROWS = NW * KT * 16;           // kv rows per workgroup
+  // 16-bit operands: Q-hat^T and dO^T are read transposed from sQ / sG
+  // (ds_read_b64_tr_b16); fp32 storage keeps explicit transposed copies.
+  constexpr bool TR = sizeof(S) == 2;
 
   __shared__ __attribute__((aligned(16))) S sQ[QS * LDQ];
-  __shared__ __attribute__((aligned(16))) S sQt[D * LDT];
+  __shared__ __attribute__((aligned(16))) S sQt[TR ? 8 : D * LDT];
   __shared__ __attribute__((aligned(16))) S sG[QS * LDQ];
-  __shared__ __attribute__((aligned(16))) S sGt[D * LDT];
+  __shared__ __attribute__((aligned(16))) S sGt[TR ? 8 : D * LDT];
   __shared__ __attribute__((aligned(16))) float sL2[QS];
   __shared__ __attribute__((aligned(16))) float sDl[QS];
 
@@ -334,10 +348,12 @@ bwd_dkdv_kernel(const BwdParams p) {
           rope_rotate8(xq[it], cs[it]);
           C::put8(&sQ[r * LDQ + 8 * cc], xq[it]);
           C::put8(&sG[r * LDQ + 8 * cc], xg[it]);
+          if constexpr (!TR) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            C::put1(&sQt[(8 * cc + e) * LDT + r], xq[it][e]);
-            C::put1(&sGt[(8 * cc + e) * LDT + r], xg[it][e]);
+            for (int e = 0; e < 8; ++e) {
+              C::put1(&sQt[(8 * cc + e) * LDT + r], xq[it][e]);
+              C::put1(&sGt[(8 * cc + e) * LDT + r], xg[it][e]);
+            }
           }
         }
       }
@@ -391,9 +407,18 @@ bwd_dkdv_kernel(const BwdParams p) {
         const Frag dsf = C::make(dsv);
 #pragma unroll
         for (int d = 0; d < DT; ++d) {
-          const Frag ag = C::lds(&sGt[(16 * d + lr) * LDT + 32 * j + 8 * lg]);
+          // A = dO^T / Q-hat^T rows 16d.., k-slot e <-> query 32j + 8lg + e (the P / dS order)
+          Frag ag, aq;
+          if constexpr (TR) {
+            const int o0 = tr_offset(32 * j + 8 * lg, 16 * d, LDQ, lr);
+            const int o1 = tr_offset(32 * j + 8 * lg + 4, 16 * d, LDQ, lr);
+            ag = C::tr(&sG[o0], &sG[o1]);
+            aq = C::tr(&sQ[o0], &sQ[o1]);
+          } else {
+            ag = C::lds(&sGt[(16 * d + lr) * LDT + 32 * j + 8 * lg]);
+            aq = C::lds(&sQt[(16 * d + lr) * LDT + 32 * j + 8 * lg]);
+          }
           dvacc[u][d] = C::mma(ag, pf, dvacc[u][d]);
-          const Frag aq = C::lds(&sQt[(16 * d + lr) * LDT + 32 * j + 8 * lg]);
           dkacc[u][d] = C::mma(aq, dsf, dkacc[u][d]);
         }
       }

@@ -156,6 +156,29 @@ __device__ __forceinline__ void rope_unrotate4(float (&g)[4], const float* __res
 }
 
 // ---------------------------------------------------------------------------
+// Transposed fragment reads from row-major LDS tiles (gfx950
+// ds_read_b64_tr_b16).  Within each 16-lane group, result lane i, element e
+// is 16-bit element (i % 4) of the 8 bytes addressed by lane 4e + i/4 of the
+// same group.  So if lane (lr, lg) addresses row R(lg) + lr/4, column
+// c0 + 4*(lr % 4) of a row-major tile M, it receives M[R(lg) + e][c0 + lr]
+// for e = 0..3: four consecutive rows of one column.  Two such reads (rows
+// R and R') give the 8 k-slots of an MFMA operand whose k index runs down
+// the columns of M, i.e. a fragment of M^T, without a transposed copy.
+// ---------------------------------------------------------------------------
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ s16x4 lds_tr4(const void* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
+}
+
+// Element offset, inside a row-major tile of pitch `ld`, that lane (lr, lg)
+// addresses so that the read yields rows r0 + e (e = 0..3) of column c0 + lr.
+__device__ __forceinline__ int tr_offset(int r0, int c0, int ld, int lr) {
+  return (r0 + (lr >> 2)) * ld + c0 + 4 * (lr & 3);
+}
+
+// ---------------------------------------------------------------------------
 // Compute-type traits: how values are kept in LDS and fed to the MFMA unit.
 //   DT_BF16: bf16 storage, one v_mfma_f32_16x16x32_bf16 per product.
 //   DT_F16 : fp16 storage, one v_mfma_f32_16x16x32_f16 per product.
@@ -189,6 +212,20 @@ template <> struct Comp<DT_BF16> {
   static __device__ __forceinline__ Frag lds(const S* p) {
     Frag f; f.v = *reinterpret_cast<const bf16x8*>(p); return f;
   }
+  // k-slots 0..3 from the transposed read at p0, 4..7 from the one at p1
+  static __device__ __forceinline__ Frag tr(const S* p0, const S* p1) {
+    const s16x4 a = lds_tr4(p0), b = lds_tr4(p1);
+    const s16x8 c = __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+    Frag f; f.v = __builtin_bit_cast(bf16x8, c); return f;
+  }
+  // store k-slots 4h..4h+3 (8 bytes)
+  static __device__ __forceinline__ void put4(S* p, const Frag& f, int h) {
+    typedef S v4 __attribute__((ext_vector_type(4)));
+    v4 t;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) t[e] = f.v[4 * h + e];
+    *reinterpret_cast<v4*>(p) = t;
+  }
   static __device__ __forceinline__ void put8(S* p, const float (&x)[8]) {
     *reinterpret_cast<bf16x8*>(p) = make(x).v;
   }
@@ -220,6 +257,20 @@ template <> struct Comp<DT_F16> {
   static __device__ __forceinline__ void put_elem(S* p, const Frag& f, int e) { *p = f.v[e]; }
   static __device__ __forceinline__ Frag lds(const S* p) {
     Frag f; f.v = *reinterpret_cast<const f16x8*>(p); return f;
+  }
+  // k-slots 0..3 from the transposed read at p0, 4..7 from the one at p1
+  static __device__ __forceinline__ Frag tr(const S* p0, const S* p1) {
+    const s16x4 a = lds_tr4(p0), b = lds_tr4(p1);
+    const s16x8 c = __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+    Frag f; f.v = __builtin_bit_cast(f16x8, c); return f;
+  }
+  // store k-slots 4h..4h+3 (8 bytes)
+  static __device__ __forceinline__ void put4(S* p, const Frag& f, int h) {
+    typedef S v4 __attribute__((ext_vector_type(4)));
+    v4 t;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) t[e] = f.v[4 * h + e];
+    *reinterpret_cast<v4*>(p) = t;
   }
   static __device__ __forceinline__ void put8(S* p, const float (&x)[8]) {
     *reinterpret_cast<f16x8*>(p) = make(x).v;
