@@ -14,12 +14,13 @@ using namespace farope;
 namespace farope {
 
 // Resident-capacity query for persistent kernels, cached per (device, kernel).
-int persistent_grid(const void* kernel, int block_threads, int items) {
+int persistent_grid(const void* kernel, int block_threads, int items, size_t dyn_lds) {
   static std::mutex mu;
   static std::unordered_map<uint64_t, int> cache;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return -1;
-  const uint64_t key = (reinterpret_cast<uint64_t>(kernel) << 8) ^ (uint64_t)(dev & 0xff);
+  const uint64_t key = ((reinterpret_cast<uint64_t>(kernel) << 8) ^ (uint64_t)(dev & 0xff)) +
+                       ((uint64_t)dyn_lds << 48);
   int cap = 0;
   {
     std::lock_guard<std::mutex> lock(mu);
@@ -29,7 +30,8 @@ int persistent_grid(const void* kernel, int block_threads, int items) {
   if (cap == 0) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -1;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block_threads, 0) != hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block_threads, dyn_lds) !=
+        hipSuccess)
       return -1;
     cap = cus * (per_cu > 0 ? per_cu : 1);
     std::lock_guard<std::mutex> lock(mu);
@@ -67,11 +69,17 @@ int check_ptr(const void* p, int es) {
 }
 
 // 16-byte vector path allowed: unit channel stride and 16-byte aligned rows.
-int vec_ok(const void* p, const int64_t s[4], int es) {
+// 16-byte vector access: unit d-stride, 16-byte aligned base and strides, a
+// non-negative row stride, and every byte offset inside one (b, h) plane
+// (row n, channel d) below 2^31, so kernels can address a plane as 64-bit
+// base + 32-bit lane offset.
+int vec_ok(const void* p, const int64_t s[4], int es, int n_rows, int head_dim) {
   if (s[3] != 1) return 0;
   if (reinterpret_cast<uintptr_t>(p) % 16) return 0;
   for (int i = 0; i < 3; ++i)
     if ((s[i] * es) % 16 != 0) return 0;
+  if (s[2] < 0) return 0;   // lane offsets are unsigned
+  if ((int64_t)(n_rows - 1) * s[2] + head_dim >= ((int64_t)1 << 31) / es) return 0;
   return 1;
 }
 
@@ -184,10 +192,10 @@ int farope_attn_fwd(const farope_attn_desc* desc, const void* q, const int64_t q
   p.rope = rope_packed;
   p.B = desc->batch; p.H = desc->heads; p.N = desc->seq_len; p.has_cls = desc->has_cls;
   p.scale_log2 = desc->softmax_scale * 1.4426950408889634f;
-  p.vec_q = vec_ok(q, q_stride, es);
-  p.vec_k = vec_ok(k, k_stride, es);
-  p.vec_v = vec_ok(v, v_stride, es);
-  p.vec_o = vec_ok(o, o_stride, es);
+  p.vec_q = vec_ok(q, q_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_k = vec_ok(k, k_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_v = vec_ok(v, v_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_o = vec_ok(o, o_stride, es, desc->seq_len, desc->head_dim);
   p.n_blk = cdiv(p.N, fwd_block_rows(desc->head_dim));
   p.n_items = p.B * p.H * p.n_blk;
   return launch_rc(launch_fwd(p, desc->io_dtype, desc->compute_dtype, desc->head_dim,
@@ -207,8 +215,8 @@ int farope_attn_bwd_preprocess(const farope_attn_desc* desc, const void* o,
   fill_common(p, desc, nullptr);
   p.o = o; p.dout = dout; p.delta = delta;
   copy4(p.so, o_stride); copy4(p.sdo, dout_stride);
-  p.vec_o = vec_ok(o, o_stride, es);
-  p.vec_do = vec_ok(dout, dout_stride, es);
+  p.vec_o = vec_ok(o, o_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_do = vec_ok(dout, dout_stride, es, desc->seq_len, desc->head_dim);
   return launch_rc(launch_bwd_pre(p, desc->io_dtype, desc->head_dim,
                                   static_cast<hipStream_t>(stream)));
 }
@@ -238,12 +246,12 @@ int farope_attn_bwd_dk_dv(const farope_attn_desc* desc, const void* q, const int
   p.lse = lse; p.delta = const_cast<float*>(delta);
   copy4(p.sq, q_stride); copy4(p.sk, k_stride); copy4(p.sv, v_stride);
   copy4(p.sdo, dout_stride); copy4(p.sdk, dk_stride); copy4(p.sdv, dv_stride);
-  p.vec_q = vec_ok(q, q_stride, es);
-  p.vec_k = vec_ok(k, k_stride, es);
-  p.vec_v = vec_ok(v, v_stride, es);
-  p.vec_do = vec_ok(dout, dout_stride, es);
-  p.vec_dk = vec_ok(dk, dk_stride, es);
-  p.vec_dv = vec_ok(dv, dv_stride, es);
+  p.vec_q = vec_ok(q, q_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_k = vec_ok(k, k_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_v = vec_ok(v, v_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_do = vec_ok(dout, dout_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_dk = vec_ok(dk, dk_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_dv = vec_ok(dv, dv_stride, es, desc->seq_len, desc->head_dim);
   p.n_blk = cdiv(p.N, bwd_dkdv_block_rows(desc->head_dim));
   return launch_rc(launch_bwd_dkdv(p, desc->io_dtype, desc->compute_dtype, desc->head_dim,
                                    static_cast<hipStream_t>(stream)));
@@ -271,11 +279,11 @@ int farope_attn_bwd_dq(const farope_attn_desc* desc, const void* q, const int64_
   p.lse = lse; p.delta = const_cast<float*>(delta);
   copy4(p.sq, q_stride); copy4(p.sk, k_stride); copy4(p.sv, v_stride);
   copy4(p.sdo, dout_stride); copy4(p.sdq, dq_stride);
-  p.vec_q = vec_ok(q, q_stride, es);
-  p.vec_k = vec_ok(k, k_stride, es);
-  p.vec_v = vec_ok(v, v_stride, es);
-  p.vec_do = vec_ok(dout, dout_stride, es);
-  p.vec_dq = vec_ok(dq, dq_stride, es);
+  p.vec_q = vec_ok(q, q_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_k = vec_ok(k, k_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_v = vec_ok(v, v_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_do = vec_ok(dout, dout_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_dq = vec_ok(dq, dq_stride, es, desc->seq_len, desc->head_dim);
   p.n_blk = cdiv(p.N, bwd_dq_block_rows(desc->head_dim));
   return launch_rc(launch_bwd_dq(p, desc->io_dtype, desc->compute_dtype, desc->head_dim, false,
                                  static_cast<hipStream_t>(stream)));
@@ -313,14 +321,14 @@ int farope_attn_bwd(const farope_attn_desc* desc, const void* q, const int64_t q
   copy4(p.sq, q_stride); copy4(p.sk, k_stride); copy4(p.sv, v_stride); copy4(p.so, o_stride);
   copy4(p.sdo, dout_stride); copy4(p.sdq, dq_stride); copy4(p.sdk, dk_stride);
   copy4(p.sdv, dv_stride);
-  p.vec_q = vec_ok(q, q_stride, es);
-  p.vec_k = vec_ok(k, k_stride, es);
-  p.vec_v = vec_ok(v, v_stride, es);
-  p.vec_o = vec_ok(o, o_stride, es);
-  p.vec_do = vec_ok(dout, dout_stride, es);
-  p.vec_dq = vec_ok(dq, dq_stride, es);
-  p.vec_dk = vec_ok(dk, dk_stride, es);
-  p.vec_dv = vec_ok(dv, dv_stride, es);
+  p.vec_q = vec_ok(q, q_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_k = vec_ok(k, k_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_v = vec_ok(v, v_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_o = vec_ok(o, o_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_do = vec_ok(dout, dout_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_dq = vec_ok(dq, dq_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_dk = vec_ok(dk, dk_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_dv = vec_ok(dv, dv_stride, es, desc->seq_len, desc->head_dim);
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const int D = desc->head_dim;
   if (fused) {

@@ -32,8 +32,8 @@ template <typename IO, int D>
 __global__ void __launch_bounds__(256) bwd_pre_kernel(const BwdParams p) {
   constexpr int CPR = D / 8;
   constexpr int RPB = 256 / CPR;
-  const int64_t grow = (int64_t)blockIdx.x * RPB + threadIdx.x / CPR;
-  const int cc = threadIdx.x % CPR;
+  const int64_t grow = (int64_t)block_id() * RPB + thread_id() / CPR;
+  const int cc = thread_id() % CPR;
   const int64_t total = (int64_t)p.B * p.H * p.N;
   float acc = 0.f;
   if (grow < total) {
@@ -77,7 +77,7 @@ bwd_dq_kernel(const BwdParams p) {
   __shared__ __attribute__((aligned(16))) S sV[KVS * LDK];
 
   const int N = p.N;
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int tile = xcd_remap(block_id(), p.n_wg);
   const int plane = tile / p.n_blk;
   const int qblk = tile - plane * p.n_blk;
   const int bb = plane / p.H, hh = plane - bb * p.H;
@@ -91,7 +91,7 @@ bwd_dq_kernel(const BwdParams p) {
   const int shift = 1 - p.has_cls;
   const int64_t prow = (int64_t)plane * N;
 
-  const int tid = threadIdx.x;
+  const int tid = thread_id();
   const int wave = tid >> 6, lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
 
@@ -145,7 +145,7 @@ bwd_dq_kernel(const BwdParams p) {
 
   for (int kvb = 0; kvb < N; kvb += KVS) {
     const int rows = min(KVS, round_up32(N - kvb));
-    if (kvb > 0) __syncthreads();
+    if (kvb > 0) lds_barrier();
     {
       float xk[ITER][8], xv[ITER][8], cs[ITER][8];
 #pragma unroll
@@ -176,7 +176,7 @@ bwd_dq_kernel(const BwdParams p) {
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
     if (!wave_active) continue;
 
     for (int j = 0; j < rows / 32; ++j) {
@@ -272,7 +272,7 @@ bwd_dkdv_kernel(const BwdParams p) {
   __shared__ __attribute__((aligned(16))) float sDl[QS];
 
   const int N = p.N;
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int tile = xcd_remap(block_id(), p.n_wg);
   const int plane = tile / p.n_blk;
   const int kblk = tile - plane * p.n_blk;
   const int bb = plane / p.H, hh = plane - bb * p.H;
@@ -286,7 +286,7 @@ bwd_dkdv_kernel(const BwdParams p) {
   const int shift = 1 - p.has_cls;
   const int64_t prow = (int64_t)plane * N;
 
-  const int tid = threadIdx.x;
+  const int tid = thread_id();
   const int wave = tid >> 6, lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
   const int kv_first = kblk * KROWS + wave * KT * 16;
@@ -323,7 +323,7 @@ bwd_dkdv_kernel(const BwdParams p) {
 
   for (int qb = 0; qb < N; qb += QS) {
     const int rows = min(QS, round_up32(N - qb));
-    __syncthreads();
+    lds_barrier();
     // ---- stage Q-hat, Q-hat^T, dO, dO^T (+ delta, LSE) for this q stage ----
     {
       float xq[ITER][8], xg[ITER][8], cs[ITER][8];
@@ -363,7 +363,7 @@ bwd_dkdv_kernel(const BwdParams p) {
         sDl[r] = gr < N ? p.delta[prow + gr] : 0.f;
       }
     }
-    __syncthreads();
+    lds_barrier();
 
     for (int j = 0; j < rows / 32; ++j) {
       float l2[8], dl[8];
@@ -491,9 +491,10 @@ hipError_t launch_bwd_pre(const BwdParams& p, int io, int D, hipStream_t st) {
 }
 
 template <typename IO, int CT, int D>
-static hipError_t dq_launch(const BwdParams& p, bool write_delta, hipStream_t st) {
+static hipError_t dq_launch(const BwdParams& p0, bool write_delta, hipStream_t st) {
   using SH = BwdShape<D>;
-  const int grid = p.B * p.H * p.n_blk;
+  BwdParams p = p0;
+  const int grid = p.n_wg = p.B * p.H * p.n_blk;
   if (write_delta)
     hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, true>),
                        dim3(grid), dim3(SH::DQ_NW * 64), 0, st, p);
@@ -504,9 +505,10 @@ static hipError_t dq_launch(const BwdParams& p, bool write_delta, hipStream_t st
 }
 
 template <typename IO, int CT, int D>
-static hipError_t dkdv_launch(const BwdParams& p, hipStream_t st) {
+static hipError_t dkdv_launch(const BwdParams& p0, hipStream_t st) {
   using SH = BwdShape<D>;
-  const int grid = p.B * p.H * p.n_blk;
+  BwdParams p = p0;
+  const int grid = p.n_wg = p.B * p.H * p.n_blk;
   hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS>), dim3(grid),
                      dim3(SH::KV_NW * 64), 0, st, p);
   return hipGetLastError();
@@ -559,7 +561,7 @@ hipError_t launch_bwd_dkdv(const BwdParams& p, int io, int ct, int D, hipStream_
 __global__ void rope_pack_kernel(const float* __restrict__ cosp, int64_t cs0, int64_t cs1,
                                  const float* __restrict__ sinp, int64_t ss0, int64_t ss1,
                                  int n_pos, int d2, float* __restrict__ out) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t i = (int64_t)block_id() * 256 + thread_id();
   const int64_t total = (int64_t)(n_pos + 1) * d2;
   if (i >= total) return;
   const int row = (int)(i / d2), pr = (int)(i - (int64_t)row * d2);

@@ -38,10 +38,20 @@ namespace farope {
 
 namespace {
 constexpr int kPlaneNW = 8;                   // waves per workgroup
-constexpr int kPlaneQS = 64;                  // query rows per stage
+constexpr int kPlaneQS = 32;                  // query rows per stage
 constexpr int kPlaneMaxN = kPlaneNW * 32;     // keys per workgroup
-constexpr int kPlaneLD = 64 + 8;              // pitch of every LDS tile (elements)
+constexpr int kPlaneLD = 64 + 8;              // pitch of the Q-hat / dO / K-hat tiles (elements)
+constexpr int kPlaneLDD = kPlaneQS + 8;       // pitch of the key-major dS^T tile (elements)
 }  // namespace
+
+// LDS copy of the RoPE table rows a plane uses, one 256-byte row (32 pairs of
+// (cos, sin)) per token.  The sixteen 16-byte chunks of token row r are
+// stored in chunk order c ^ (r & 15): sixteen lanes reading the same chunk of
+// sixteen consecutive rows, and eight lanes reading a whole row next to eight
+// reading the following row, both touch every bank once.
+__device__ __forceinline__ f32x4 tab_chunk(const float* t, int row, int c) {
+  return *reinterpret_cast<const f32x4*>(t + ((row << 4) + (c ^ (row & 15))) * 4);
+}
 
 // VEC: every tensor of the call allows 16-byte vector access (decided on the
 // host); the generic instantiation gathers element by element instead.
@@ -51,36 +61,25 @@ bwd_plane_kernel(const BwdParams p) {
   using C = Comp<CT>;
   using S = typename C::S;
   using Frag = typename C::Frag;
-  constexpr int D = 64, D2 = 32, LD = kPlaneLD, QS = kPlaneQS;
+  constexpr int LD = kPlaneLD, LDD = kPlaneLDD, QS = kPlaneQS;
   static_assert(sizeof(S) == 2, "the plane kernel stores 16-bit operands");
 
-  __shared__ __attribute__((aligned(16))) S sQ[2][QS * LD];          // Q-hat rows of a stage
-  __shared__ __attribute__((aligned(16))) S sG[2][QS * LD];          // dO rows of a stage
-  __shared__ __attribute__((aligned(16))) S sdS[2][kPlaneMaxN * LD]; // dS^T [key][query]
-  __shared__ __attribute__((aligned(16))) S sK[kPlaneMaxN * LD];     // K-hat rows of the plane
+  __shared__ __attribute__((aligned(16))) S sQ[2][QS * LD];           // Q-hat rows of a stage
+  __shared__ __attribute__((aligned(16))) S sG[2][QS * LD];           // dO rows of a stage
+  __shared__ __attribute__((aligned(16))) S sdS[2][kPlaneMaxN * LDD]; // dS^T [key][query]
+  __shared__ __attribute__((aligned(16))) S sK[kPlaneMaxN * LD];      // K-hat rows of the plane
   __shared__ __attribute__((aligned(16))) float sL2[2][QS];
   __shared__ __attribute__((aligned(16))) float sDl[2][QS];
+  extern __shared__ __attribute__((aligned(16))) float sTab[];        // N rows x 64 floats
 
   const int N = p.N;
+  const int planes = p.B * p.H;
   const bool vec_q = VEC || p.vec_q, vec_k = VEC || p.vec_k, vec_v = VEC || p.vec_v;
   const bool vec_o = VEC || p.vec_o, vec_do = VEC || p.vec_do, vec_dq = VEC || p.vec_dq;
   const bool vec_dk = VEC || p.vec_dk, vec_dv = VEC || p.vec_dv;
-  const int plane = xcd_remap(blockIdx.x, gridDim.x);
-  const int bb = plane / p.H, hh = plane - bb * p.H;
-  const IO* __restrict__ Q = static_cast<const IO*>(p.q) + bb * p.sq[0] + hh * p.sq[1];
-  const IO* __restrict__ K = static_cast<const IO*>(p.k) + bb * p.sk[0] + hh * p.sk[1];
-  const IO* __restrict__ V = static_cast<const IO*>(p.v) + bb * p.sv[0] + hh * p.sv[1];
-  const IO* __restrict__ O = static_cast<const IO*>(p.o) + bb * p.so[0] + hh * p.so[1];
-  const IO* __restrict__ G = static_cast<const IO*>(p.dout) + bb * p.sdo[0] + hh * p.sdo[1];
-  IO* __restrict__ dQ = static_cast<IO*>(p.dq) + bb * p.sdq[0] + hh * p.sdq[1];
-  IO* __restrict__ dK = static_cast<IO*>(p.dk) + bb * p.sdk[0] + hh * p.sdk[1];
-  IO* __restrict__ dV = static_cast<IO*>(p.dv) + bb * p.sdv[0] + hh * p.sdv[1];
-  const float* __restrict__ tab = p.rope;
-  const float* __restrict__ lse = p.lse + (int64_t)plane * N;
-  const int shift = 1 - p.has_cls;
   const float c2 = p.scale_log2;
 
-  const int tid = threadIdx.x;
+  const int tid = thread_id();
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (SGPR)
   const int lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
@@ -89,196 +88,285 @@ bwd_plane_kernel(const BwdParams p) {
   const int nstages = (N + QS - 1) / QS;
   const int kw = 32 * wave;                                    // first key of this wave
   const int nu = (kw < N) + (kw + 16 < N);                     // active 16-key subtiles
+  const int dd = wave & 3;    // head-dim slice 16dd .. 16dd+15 of this wave's dQ tile
+  const int qt = wave >> 2;   // and its 16-query subtile of a stage
 
-  // ---- stage staging: thread t carries row t/8, channels 8*(t%8) .. +7 of Q, dO, O ----
-  const int sr = tid >> 3, sc = tid & 7;
-  const IO* q_st = Q + sr * p.sq[2] + 8 * sc * p.sq[3];
-  const IO* g_st = G + sr * p.sdo[2] + 8 * sc * p.sdo[3];
-  const IO* o_st = O + sr * p.so[2] + 8 * sc * p.so[3];
+  // Persistent: workgroup g handles planes g, g + G, g + 2G, ... (G = grid),
+  // dealt XCD-major so that consecutive planes of an XCD share its L2.
+  const int pos = xcd_remap(block_id(), p.n_wg);
+  auto item_of = [&](int it) {
+    const int item = it * p.n_wg + pos;
+    return item < planes ? item : -1;
+  };
+  auto base = [&](const void* b, const int64_t* st, int plane) {
+    const int bb = plane / p.H, hh = plane - bb * p.H;
+    return static_cast<const IO*>(b) + bb * st[0] + hh * st[1];
+  };
+  // VEC: the host guarantees unit d-stride, 16-byte alignment and in-plane
+  // byte offsets below 2^31.  Tensors are then read and written through
+  // buffer descriptors over rows 0 .. N-1 of the plane (SGPRs), with 32-bit
+  // lane byte offsets fixed for the whole kernel and uniform per-stage
+  // offsets: no 64-bit address arithmetic per lane, and rows >= N read as 0.
+  // Otherwise: generic strided 64-bit addressing.
+  constexpr unsigned ES = sizeof(IO);
+  auto rsrc = [&](const void* b, const int64_t* st, int plane) {
+    return make_rsrc(base(b, st, plane), (unsigned)(((int64_t)(N - 1) * st[2] + 64) * ES));
+  };
+  auto boff = [&](const int64_t* st, int row, int col) {   // lane byte offset (VEC)
+    return (unsigned)((row * (int)st[2] + col) * (int)ES);
+  };
+
+  // ---- stage staging: thread t < 256 carries row t/8, channels 8*(t%8) .. +7
+  //      of Q, dO and O; threads 256 .. 256+QS-1 carry the stage's LSE ----
   Raw8<IO> pq, pg, po;
-  float pcs[8];
   float plse = 0.f;
-  auto prefetch = [&](int qb) {
-    const int gr = qb + sr;
-    if (gr < N) {
-      pq = load_raw8(q_st + qb * p.sq[2], p.sq[3], vec_q);
-      pg = load_raw8(g_st + qb * p.sdo[2], p.sdo[3], vec_do);
-      po = load_raw8(o_st + qb * p.so[2], p.so[3], vec_o);
-      rope_load4(tab, gr + shift, D2, 4 * sc, pcs);
-    } else {
-      pq = pg = po = zero_raw8<IO>();
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pcs[e] = 0.f;
-    }
-    if (tid < QS) plse = qb + tid < N ? lse[qb + tid] * kLog2e : INFINITY;
-  };
-  auto commit = [&](int buf) {
-    float x[8], g[8], o[8];
-    unpack8(pq, x);
-    unpack8(pg, g);
-    unpack8(po, o);
-    rope_rotate8(x, pcs);
-    C::put8(&sQ[buf][sr * LD + 8 * sc], x);
-    C::put8(&sG[buf][sr * LD + 8 * sc], g);
-    float d = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) d += g[e] * o[e];
-    // the 8 chunks of a row are 8 consecutive lanes
-    d += __shfl_xor(d, 1);
-    d += __shfl_xor(d, 2);
-    d += __shfl_xor(d, 4);
-    if (sc == 0) sDl[buf][sr] = d;
-    if (tid < QS) sL2[buf][tid] = plse;
-  };
-
-  prefetch(0);
-
-  // ---- own keys: K-hat and V rows as B-operands; K-hat rows also go to sK
-  //      (row-major, all 256 rows, zero beyond N) ----
-  Frag kf[2][2], vf[2][2];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int row = kw + 16 * u + lr;
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int c0 = 32 * s + 8 * lg;
-      float x[8], y[8];
-      if (row < N) {
-        load8(K + row * p.sk[2] + c0 * p.sk[3], p.sk[3], vec_k, x);
-        float cs[8];
-        rope_load4(tab, row + shift, D2, c0 / 2, cs);
-        rope_rotate8(x, cs);
-        load8(V + row * p.sv[2] + c0 * p.sv[3], p.sv[3], vec_v, y);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = y[e] = 0.f;
+  const int ssr = (tid >> 3) & 31, ssc = tid & 7;   // staging row / chunk of this thread
+  unsigned bq = 0, bg = 0, bo = 0;
+  if constexpr (VEC) {
+    bq = boff(p.sq, ssr, 8 * ssc);
+    bg = boff(p.sdo, ssr, 8 * ssc);
+    bo = boff(p.so, ssr, 8 * ssc);
+  }
+  auto prefetch = [&](int plane, int qb) __attribute__((always_inline)) {
+    if constexpr (VEC) {
+      if (tid < 256) {   // waves 0..3 (wave-uniform)
+        pq = buf_load8<IO>(rsrc(p.q, p.sq, plane), bq, (unsigned)(qb * (int)p.sq[2] * (int)ES));
+        pg = buf_load8<IO>(rsrc(p.dout, p.sdo, plane), bg, (unsigned)(qb * (int)p.sdo[2] * (int)ES));
+        po = buf_load8<IO>(rsrc(p.o, p.so, plane), bo, (unsigned)(qb * (int)p.so[2] * (int)ES));
       }
-      kf[u][s] = C::make(x);
-      vf[u][s] = C::make(y);
-      *reinterpret_cast<decltype(kf[u][s].v)*>(&sK[row * LD + c0]) = kf[u][s].v;
+    } else {
+      const int t = opaque(tid), sr = (t >> 3) & 31, sc = t & 7, gr = qb + sr;
+      if (t < 256 && gr < N) {
+        pq = load_raw8(base(p.q, p.sq, plane) + gr * p.sq[2] + 8 * sc * p.sq[3], p.sq[3], vec_q);
+        pg = load_raw8(base(p.dout, p.sdo, plane) + gr * p.sdo[2] + 8 * sc * p.sdo[3], p.sdo[3], vec_do);
+        po = load_raw8(base(p.o, p.so, plane) + gr * p.so[2] + 8 * sc * p.so[3], p.so[3], vec_o);
+      } else {
+        pq = pg = po = zero_raw8<IO>();
+      }
+    }
+    const int lt = tid - 256;
+    if (lt >= 0 && lt < QS) {
+      const float* l = p.lse + (int64_t)plane * N + qb;
+      plse = qb + lt < N ? l[lt] * kLog2e : INFINITY;
+    }
+  };
+  auto commit = [&](int buf, int qb) __attribute__((always_inline)) {
+    const int t = tid, sr = ssr, sc = ssc;
+    if (t < 256) {
+      float x[8], g[8], o[8];
+      unpack8(pq, x);
+      unpack8(pg, g);
+      unpack8(po, o);
+      // Q-hat = R q (rows >= N are zero either way)
+      const int row = min(qb + sr, N - 1);
+      const f32x4 c0 = tab_chunk(sTab, row, 2 * sc), c1 = tab_chunk(sTab, row, 2 * sc + 1);
+      const float cs[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+      rope_rotate8(x, cs);
+      C::put8(&sQ[buf][sr * LD + 8 * sc], x);
+      C::put8(&sG[buf][sr * LD + 8 * sc], g);
+      // delta = rowsum(dO * O); the 8 chunks of a row are 8 consecutive lanes
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d += g[e] * o[e];
+      d += __shfl_xor(d, 1);
+      d += __shfl_xor(d, 2);
+      d += __shfl_xor(d, 4);
+      if (sc == 0) sDl[buf][sr] = d;
+    } else if (t - 256 < QS) {
+      sL2[buf][t - 256] = plse;
+    }
+  };
+
+  // ---- own keys kw + 16u + lr: raw K / V row segments in flight ----
+  Raw8<IO> rk[2][2], rv[2][2];
+  // VEC lane byte offsets: K / V at (row kw + 16u + lr, channel 8lg); dK / dV
+  // at (row kw + 16u + lr, channel 4lg)
+  unsigned bk[2] = {0, 0}, bv[2] = {0, 0}, bdk[2] = {0, 0}, bdv[2] = {0, 0};
+  if constexpr (VEC) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      bk[u] = boff(p.sk, kw + 16 * u + lr, 8 * lg);
+      bv[u] = boff(p.sv, kw + 16 * u + lr, 8 * lg);
+      bdk[u] = boff(p.sdk, kw + 16 * u + lr, 4 * lg);
+      bdv[u] = boff(p.sdv, kw + 16 * u + lr, 4 * lg);
     }
   }
-  commit(0);
-
-  f32x4 dvacc[2][4], dkacc[2][4];
+  auto prefetch_kv = [&](int plane) __attribute__((always_inline)) {
+    if constexpr (VEC) {
+      const auto rK = rsrc(p.k, p.sk, plane), rV = rsrc(p.v, p.sv, plane);
 #pragma unroll
-  for (int u = 0; u < 2; ++u)
+      for (int u = 0; u < 2; ++u)
 #pragma unroll
-    for (int d = 0; d < 4; ++d) dvacc[u][d] = dkacc[u][d] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int dd = wave & 3;   // head-dim slice 16dd .. 16dd+15 of this wave's dQ tiles
-
-  // ---- dQ of one finished stage from its dS^T tile ----
-  auto dq_stage = [&](int sp) {
-    const int buf = sp & 1;
-    const int qb = sp * QS;
-    const int rows = min(QS, round_up32(N - qb));
-    const int qt0 = 2 * (wave >> 2);                  // this wave's two 16-query subtiles
-    const int nq = (16 * qt0 < rows) + (16 * qt0 + 16 < rows);
-    auto sweep = [&](auto nqc) {
-      constexpr int NQ = decltype(nqc)::value;
-      f32x4 acc[NQ];
+        for (int s = 0; s < 2; ++s) {
+          rk[u][s] = buf_load8<IO>(rK, bk[u], 32 * s * ES);
+          rv[u][s] = buf_load8<IO>(rV, bv[u], 32 * s * ES);
+        }
+    } else {
+      const int lane = opaque(tid & 63), lr = lane & 15, lg = lane >> 4;
 #pragma unroll
-      for (int i = 0; i < NQ; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int u = 0; u < 2; ++u) {
+        const int row = kw + 16 * u + lr;
 #pragma unroll
-      for (int kb = 0; kb < kPlaneMaxN / 32; ++kb) {
-        if (kb < nkb) {
-          // A = K-hat^T rows 16dd.., k = keys 32kb + 8lg + (0..7)
-          const Frag a = C::tr(&sK[tr_offset(32 * kb + 8 * lg, 16 * dd, LD, lr)],
-                               &sK[tr_offset(32 * kb + 8 * lg + 4, 16 * dd, LD, lr)]);
-#pragma unroll
-          for (int i = 0; i < NQ; ++i) {
-            const S* t = &sdS[buf][0];
-            const int c0 = 16 * (qt0 + i);
-            const Frag b = C::tr(t + tr_offset(32 * kb + 8 * lg, c0, LD, lr),
-                                 t + tr_offset(32 * kb + 8 * lg + 4, c0, LD, lr));
-            acc[i] = C::mma(a, b, acc[i]);
+        for (int s = 0; s < 2; ++s) {
+          const int c0 = 32 * s + 8 * lg;
+          if (row < N) {
+            rk[u][s] = load_raw8(base(p.k, p.sk, plane) + row * p.sk[2] + c0 * p.sk[3], p.sk[3], vec_k);
+            rv[u][s] = load_raw8(base(p.v, p.sv, plane) + row * p.sv[2] + c0 * p.sv[3], p.sv[3], vec_v);
+          } else {
+            rk[u][s] = rv[u][s] = zero_raw8<IO>();
           }
         }
       }
+    }
+  };
+  // K-hat and V rows as B-operands; K-hat rows also go to sK (all 256 rows, zero beyond N)
+  Frag kf[2][2], vf[2][2];
+  auto commit_kv = [&]() __attribute__((always_inline)) {
+    const int lane = opaque(tid & 63), lr = lane & 15, lg = lane >> 4;
 #pragma unroll
-      for (int i = 0; i < NQ; ++i) {
-        const int row = qb + 16 * (qt0 + i) + lr;
-        if (row < N) {
-          float g4[4];
+    for (int u = 0; u < 2; ++u) {
+      const int row = min(kw + 16 * u + lr, N - 1);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) g4[r] = acc[i][r] * p.scale;
-          rope_unrotate4(g4, tab, row + shift, D2, 8 * dd + 2 * lg);
-          store4(dQ + row * p.sdq[2] + (16 * dd + 4 * lg) * p.sdq[3], p.sdq[3], vec_dq, g4);
-        }
+      for (int s = 0; s < 2; ++s) {
+        float x[8], y[8];
+        const f32x4 t0 = tab_chunk(sTab, row, 8 * s + 2 * lg), t1 = tab_chunk(sTab, row, 8 * s + 2 * lg + 1);
+        const float cs[8] = {t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]};
+        unpack8(rk[u][s], x);
+        unpack8(rv[u][s], y);
+        rope_rotate8(x, cs);
+        kf[u][s] = C::make(x);
+        vf[u][s] = C::make(y);
+        *reinterpret_cast<decltype(kf[u][s].v)*>(&sK[(kw + 16 * u + lr) * LD + 32 * s + 8 * lg]) =
+            kf[u][s].v;
       }
-    };
-    if (nq == 2) {
-      sweep(std::integral_constant<int, 2>{});
-    } else if (nq == 1) {
-      sweep(std::integral_constant<int, 1>{});
     }
   };
 
-  // ---- S, dP, P, dS, dV, dK for the wave's first NUA subtiles over one stage ----
-  auto sweep_keys = [&](auto nuc, int buf, int rows) {
+  // S-accumulator start per own subtile: 0 for keys < N, -inf beyond (all 4
+  // rows of the lane's column are the same key)
+  f32x4 kmask[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const float m = kw + 16 * u + lr < N ? 0.f : -INFINITY;
+    kmask[u] = f32x4{m, m, m, m};
+  }
+
+  f32x4 dvacc[2][4], dkacc[2][4];
+
+  // ---- dQ of one finished stage from its dS^T tile: this wave's 16x16 tile
+  //      dQ-hat^T[16dd.., 16qt..] = K-hat^T dS^T, un-rotated and stored.
+  //      NKB = number of 32-key blocks (straight-line code, no per-block branch) ----
+  // VEC lane byte offset of this lane's dQ element (row 16qt + lr of a stage, channel 16dd + 4lg)
+  const unsigned bdq = VEC ? boff(p.sdq, 16 * qt + lr, 16 * dd + 4 * lg) : 0u;
+  auto dq_stage = [&](auto nkbc, int plane, int sp) __attribute__((always_inline)) {
+    constexpr int NKB = decltype(nkbc)::value;
+    const int lane = opaque(tid & 63), lr = lane & 15, lg = lane >> 4;
+    const int buf = sp & 1;
+    const int qb = sp * QS;
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    // lane parts of the transposed-read offsets (rows 8lg + lr/4); the key
+    // block adds a compile-time constant (folded into the instruction)
+    const S* ka = &sK[tr_offset(8 * lg, 16 * dd, LD, lr)];
+    const S* db = &sdS[buf][tr_offset(8 * lg, 16 * qt, LDD, lr)];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      // A = K-hat^T rows 16dd.., B = dS^T columns 16qt..; k = keys 32kb + 8lg + (0..7)
+      const Frag a = C::tr(ka + 32 * kb * LD, ka + (32 * kb + 4) * LD);
+      const Frag b = C::tr(db + 32 * kb * LDD, db + (32 * kb + 4) * LDD);
+      acc = C::mma(a, b, acc);
+    }
+    const int row = qb + 16 * qt + lr;
+    if (row < N) {
+      const f32x4 t = tab_chunk(sTab, row, 4 * dd + lg);   // pairs 8dd + 2lg + (0, 1)
+      float g4[4];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {   // g = R^T g-hat
+        const float e = acc[2 * r] * p.scale, o = acc[2 * r + 1] * p.scale;
+        const float c = t[2 * r], sn = t[2 * r + 1];
+        g4[2 * r] = e * c + o * sn;
+        g4[2 * r + 1] = o * c - e * sn;
+      }
+      if constexpr (VEC) {
+        buf_store4<IO>(rsrc(p.dq, p.sdq, plane), bdq, (unsigned)(qb * (int)p.sdq[2] * (int)ES), g4);
+      } else {
+        IO* __restrict__ dQ = const_cast<IO*>(base(p.dq, p.sdq, plane));
+        store4(dQ + row * p.sdq[2] + (16 * dd + 4 * lg) * p.sdq[3], p.sdq[3], vec_dq, g4);
+      }
+    }
+  };
+  auto dq = [&](int plane, int sp) __attribute__((always_inline)) {
+    switch (nkb) {
+      case 1: dq_stage(std::integral_constant<int, 1>{}, plane, sp); break;
+      case 2: dq_stage(std::integral_constant<int, 2>{}, plane, sp); break;
+      case 3: dq_stage(std::integral_constant<int, 3>{}, plane, sp); break;
+      case 4: dq_stage(std::integral_constant<int, 4>{}, plane, sp); break;
+      case 5: dq_stage(std::integral_constant<int, 5>{}, plane, sp); break;
+      case 6: dq_stage(std::integral_constant<int, 6>{}, plane, sp); break;
+      case 7: dq_stage(std::integral_constant<int, 7>{}, plane, sp); break;
+      default: dq_stage(std::integral_constant<int, 8>{}, plane, sp); break;
+    }
+  };
+
+  // ---- S, dP, P, dS, dV, dK for the wave's first NUA subtiles over one
+  //      32-query stage (query rows in natural order, see above) ----
+  auto sweep_keys = [&](auto nuc, int buf) __attribute__((always_inline)) {
     constexpr int NUA = decltype(nuc)::value;
     const S* q = &sQ[buf][0];
     const S* g = &sG[buf][0];
     S* ds = &sdS[buf][0];
     if constexpr (NUA > 0) {
+      Frag pf[NUA], dsf[NUA];
 #pragma unroll
-    for (int j = 0; j < QS / 32; ++j) {
-      if (32 * j < rows) {
-        Frag pf[NUA], dsf[NUA];
+      for (int h = 0; h < 2; ++h) {
+        const int q0 = 16 * h + 4 * lg;   // queries q0 .. q0+3 in this lane
+        const f32x4 l2 = *reinterpret_cast<const f32x4*>(&sL2[buf][q0]);
+        const f32x4 dl = *reinterpret_cast<const f32x4*>(&sDl[buf][q0]);
+        // accumulators start at the key mask (S) and at -delta (dP), so that
+        // P = exp2(S*c2 - l2) is 0 for keys >= N and dP - delta needs no extra op
+        f32x4 sacc[NUA], pacc[NUA];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          f32x4 sacc[NUA], pacc[NUA];
+        for (int u = 0; u < NUA; ++u) {
+          sacc[u] = kmask[u];
+          pacc[u] = -dl;
+        }
+        const int qr = 16 * h + lr;
 #pragma unroll
-          for (int u = 0; u < NUA; ++u) sacc[u] = pacc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-          const int qr = 32 * j + 16 * h + lr;
-#pragma unroll
-          for (int s = 0; s < 2; ++s) {
-            const Frag a = C::lds(q + qr * LD + 32 * s + 8 * lg);
-            const Frag b = C::lds(g + qr * LD + 32 * s + 8 * lg);
-#pragma unroll
-            for (int u = 0; u < NUA; ++u) {
-              sacc[u] = C::mma(a, kf[u][s], sacc[u]);
-              pacc[u] = C::mma(b, vf[u][s], pacc[u]);
-            }
-          }
-          const int q0 = 32 * j + 16 * h + 4 * lg;   // queries q0 .. q0+3 in this lane
-          const f32x4 l2 = *reinterpret_cast<const f32x4*>(&sL2[buf][q0]);
-          const f32x4 dl = *reinterpret_cast<const f32x4*>(&sDl[buf][q0]);
+        for (int s = 0; s < 2; ++s) {
+          const Frag a = C::lds(q + qr * LD + 32 * s + 8 * lg);
+          const Frag b = C::lds(g + qr * LD + 32 * s + 8 * lg);
 #pragma unroll
           for (int u = 0; u < NUA; ++u) {
-            const int kv0 = kw + 16 * u;
-            float pv[4], dsv[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) pv[i] = fast_exp2(__builtin_fmaf(sacc[u][i], c2, -l2[i]));
-            if (kv0 + 16 > N) {   // wave-uniform: only the subtile holding key N-1 masks
-#pragma unroll
-              for (int i = 0; i < 4; ++i) pv[i] = kv0 + lr < N ? pv[i] : 0.f;
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) dsv[i] = pv[i] * (pacc[u][i] - dl[i]);
-            C::set2(pf[u], 2 * h, pv[0], pv[1]);
-            C::set2(pf[u], 2 * h + 1, pv[2], pv[3]);
-            C::set2(dsf[u], 2 * h, dsv[0], dsv[1]);
-            C::set2(dsf[u], 2 * h + 1, dsv[2], dsv[3]);
-            C::put4(ds + (kv0 + lr) * LD + q0, dsf[u], h);
+            sacc[u] = C::mma(a, kf[u][s], sacc[u]);
+            pacc[u] = C::mma(b, vf[u][s], pacc[u]);
           }
         }
-        // dV^T += dO^T P ; dK-hat^T += Q-hat^T dS  (k = queries 32j + 16h + 4lg + e)
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const int o0 = tr_offset(32 * j + 4 * lg, 16 * d, LD, lr);
-          const int o1 = tr_offset(32 * j + 16 + 4 * lg, 16 * d, LD, lr);
-          const Frag ag = C::tr(g + o0, g + o1);
-          const Frag aq = C::tr(q + o0, q + o1);
+        for (int u = 0; u < NUA; ++u) {
+          float pv[4], dsv[4];
 #pragma unroll
-          for (int u = 0; u < NUA; ++u) {
-            dvacc[u][d] = C::mma(ag, pf[u], dvacc[u][d]);
-            dkacc[u][d] = C::mma(aq, dsf[u], dkacc[u][d]);
-          }
+          for (int i = 0; i < 4; ++i) pv[i] = fast_exp2(__builtin_fmaf(sacc[u][i], c2, -l2[i]));
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dsv[i] = pv[i] * pacc[u][i];
+          C::set2(pf[u], 2 * h, pv[0], pv[1]);
+          C::set2(pf[u], 2 * h + 1, pv[2], pv[3]);
+          C::set2(dsf[u], 2 * h, dsv[0], dsv[1]);
+          C::set2(dsf[u], 2 * h + 1, dsv[2], dsv[3]);
+          C::put4(ds + (kw + 16 * u + lr) * LDD + q0, dsf[u], h);
         }
       }
-    }
+      // dV^T += dO^T P ; dK-hat^T += Q-hat^T dS  (k = queries 16h + 4lg + e)
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const int o0 = tr_offset(4 * lg, 0, LD, lr) + 16 * d;   // rows 4lg + e
+        const int o1 = o0 + 16 * LD;                            // rows 16 + 4lg + e
+        const Frag ag = C::tr(g + o0, g + o1);
+        const Frag aq = C::tr(q + o0, q + o1);
+#pragma unroll
+        for (int u = 0; u < NUA; ++u) {
+          dvacc[u][d] = C::mma(ag, pf[u], dvacc[u][d]);
+          dkacc[u][d] = C::mma(aq, dsf[u], dkacc[u][d]);
+        }
+      }
     }
     // subtiles without keys < N still cover columns < nkv32 of dS^T: zero them
 #pragma unroll
@@ -286,61 +374,121 @@ bwd_plane_kernel(const BwdParams p) {
       const int kv0 = kw + 16 * u;
       if (kv0 < nkv32) {
         const Frag z = C::zero();
-#pragma unroll
-        for (int j = 0; j < QS / 32; ++j)
-          if (32 * j < rows) {
-            C::put4(ds + (kv0 + lr) * LD + 32 * j + 4 * lg, z, 0);
-            C::put4(ds + (kv0 + lr) * LD + 32 * j + 16 + 4 * lg, z, 0);
-          }
+        C::put4(ds + (kv0 + lr) * LDD + 4 * lg, z, 0);
+        C::put4(ds + (kv0 + lr) * LDD + 16 + 4 * lg, z, 0);
       }
     }
   };
 
-  for (int st = 0; st < nstages; ++st) {
-    const int buf = st & 1;
-    const int qb = st * QS;
-    if (st > 0) commit(buf);
-    __syncthreads();
-    if (st + 1 < nstages) prefetch(qb + QS);
-    if (st > 0) dq_stage(st - 1);
-    const int rows = min(QS, round_up32(N - qb));
-    if (nu == 2) {
-      sweep_keys(std::integral_constant<int, 2>{}, buf, rows);
-    } else if (nu == 1) {
-      sweep_keys(std::integral_constant<int, 1>{}, buf, rows);
-    } else {
-      sweep_keys(std::integral_constant<int, 0>{}, buf, rows);
+  int it = 0;
+  int plane = item_of(0);
+  if (plane < 0) return;
+  prefetch(plane, 0);
+  prefetch_kv(plane);
+  {
+    // table rows shift .. N-1+shift of the packed table -> sTab (token order, swizzled)
+    const int shift = 1 - p.has_cls;
+    const f32x4* src = reinterpret_cast<const f32x4*>(p.rope) + shift * 16;
+    for (int i = tid; i < N * 16; i += kPlaneNW * 64) {
+      const int r = i >> 4, c = i & 15;
+      *reinterpret_cast<f32x4*>(&sTab[((r << 4) + (c ^ (r & 15))) * 4]) = src[i];
     }
   }
-  __syncthreads();
-  dq_stage(nstages - 1);
+  while (plane >= 0) {
+    const int nxt = item_of(it + 1);
+    // the previous plane's dQ tail has finished reading sK / sdS (and, on the
+    // first plane, the table copy is visible)
+    lds_barrier();
+    commit_kv();
+    commit(0, 0);
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int d = 0; d < 4; ++d) dvacc[u][d] = dkacc[u][d] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // ---- epilogue: lane holds dV / dK-hat of key kv0 + lr, channels 16d + 4lg + (0..3) ----
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int row = kw + 16 * u + lr;
-    if (u < nu && row < N) {
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        float v4[4], g4[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) { v4[r] = dvacc[u][d][r]; g4[r] = dkacc[u][d][r] * p.scale; }
-        store4(dV + row * p.sdv[2] + (16 * d + 4 * lg) * p.sdv[3], p.sdv[3], vec_dv, v4);
-        rope_unrotate4(g4, tab, row + shift, D2, 8 * d + 2 * lg);
-        store4(dK + row * p.sdk[2] + (16 * d + 4 * lg) * p.sdk[3], p.sdk[3], vec_dk, g4);
+    for (int st = 0; st < nstages; ++st) {
+      const int buf = st & 1;
+      const int qb = st * QS;
+      if (st > 0) commit(buf, qb);
+      lds_barrier();
+      // next stage, or the next plane's first stage (the last plane re-reads its
+      // own first stage: unconditional loads keep these registers' live
+      // ranges inside one loop iteration)
+      if (st + 1 < nstages) {
+        prefetch(plane, qb + QS);
+      } else {
+        prefetch(nxt >= 0 ? nxt : plane, 0);
+      }
+      if (st > 0) dq(plane, st - 1);
+      if (nu == 2) {
+        sweep_keys(std::integral_constant<int, 2>{}, buf);
+      } else if (nu == 1) {
+        sweep_keys(std::integral_constant<int, 1>{}, buf);
+      } else {
+        sweep_keys(std::integral_constant<int, 0>{}, buf);
       }
     }
+
+    // kf / vf are dead: start the next plane's own K / V rows, then finish this
+    // plane: dQ of the last stage, dK / dV
+    prefetch_kv(nxt >= 0 ? nxt : plane);
+    lds_barrier();
+    dq(plane, nstages - 1);
+    // ---- dK / dV epilogue: lane holds dV /
+    //      dK-hat of key kw + 16u + lr, channels 16d + 4lg + (0..3) ----
+    {
+      const int lane = VEC ? tid & 63 : opaque(tid & 63), lr = lane & 15, lg = lane >> 4;
+      IO* __restrict__ dK = const_cast<IO*>(base(p.dk, p.sdk, plane));
+      IO* __restrict__ dV = const_cast<IO*>(base(p.dv, p.sdv, plane));
+      const auto rdK = rsrc(p.dk, p.sdk, plane), rdV = rsrc(p.dv, p.sdv, plane);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int row = kw + 16 * u + lr;
+        if (u < nu && row < N) {
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            float v4[4], g4[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v4[r] = dvacc[u][d][r];
+            if constexpr (VEC)
+              buf_store4<IO>(rdV, bdv[u], 16 * d * ES, v4);
+            else
+              store4(dV + row * p.sdv[2] + (16 * d + 4 * lg) * p.sdv[3], p.sdv[3], vec_dv, v4);
+            const f32x4 t = tab_chunk(sTab, row, 4 * d + lg);   // pairs 8d + 2lg + (0, 1)
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {   // g = R^T g-hat
+              const float e = dkacc[u][d][2 * r] * p.scale, o = dkacc[u][d][2 * r + 1] * p.scale;
+              const float c = t[2 * r], sn = t[2 * r + 1];
+              g4[2 * r] = e * c + o * sn;
+              g4[2 * r + 1] = o * c - e * sn;
+            }
+            if constexpr (VEC)
+              buf_store4<IO>(rdK, bdk[u], 16 * d * ES, g4);
+            else
+              store4(dK + row * p.sdk[2] + (16 * d + 4 * lg) * p.sdk[3], p.sdk[3], vec_dk, g4);
+          }
+        }
+      }
+    }
+    plane = nxt;
+    ++it;
   }
 }
 
 int bwd_fused_rows() { return kPlaneMaxN; }
 
 template <typename IO, int CT>
-static hipError_t fused_launch(const BwdParams& p, hipStream_t st) {
+static hipError_t fused_launch(const BwdParams& p0, hipStream_t st) {
+  BwdParams p = p0;
   const bool vec = p.vec_q && p.vec_k && p.vec_v && p.vec_o && p.vec_do && p.vec_dq && p.vec_dk &&
                    p.vec_dv;
   auto kern = vec ? bwd_plane_kernel<IO, CT, true> : bwd_plane_kernel<IO, CT, false>;
-  hipLaunchKernelGGL(kern, dim3(p.B * p.H), dim3(kPlaneNW * 64), 0, st, p);
+  const size_t tab_bytes = (size_t)p.N * 64 * sizeof(float);   // LDS copy of the RoPE rows
+  const int grid = persistent_grid(reinterpret_cast<const void*>(kern), kPlaneNW * 64, p.B * p.H,
+                                   tab_bytes);
+  if (grid <= 0) return hipErrorInvalidValue;
+  p.n_wg = grid;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kPlaneNW * 64), tab_bytes, st, p);
   return hipGetLastError();
 }
 

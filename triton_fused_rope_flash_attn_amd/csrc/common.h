@@ -118,6 +118,56 @@ __device__ __forceinline__ void store4(IO* __restrict__ p, int64_t sd, bool vec,
 }
 
 // ---------------------------------------------------------------------------
+// Buffer (descriptor) access for vectorisable tensors: a 128-bit resource in
+// SGPRs holds the base address and the byte size of the addressed range; each
+// lane supplies a 32-bit byte offset and the wave a uniform one, so no 64-bit
+// address arithmetic runs per lane.  Loads past the range return 0 and stores
+// past it are dropped.
+// ---------------------------------------------------------------------------
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+constexpr int kBufWord3 = 0x00020000;   // raw buffer, 32-bit data format (gfx9 family)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufWord3);
+}
+
+// 8 elements at byte offset voff + soff
+template <typename IO>
+__device__ __forceinline__ Raw8<IO> buf_load8(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff) {
+  Raw8<IO> x;
+  if constexpr (sizeof(IO) == 2) {
+    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    __builtin_memcpy(&x, &a, 16);
+  } else {
+    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, soff, 0);
+    __builtin_memcpy(&x, &a, 16);
+    __builtin_memcpy(reinterpret_cast<char*>(&x) + 16, &b, 16);
+  }
+  return x;
+}
+
+// 4 elements (converted to IO) at byte offset voff + soff
+template <typename IO>
+__device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff,
+                                           const float (&x)[4]) {
+  if constexpr (sizeof(IO) == 2) {
+    typedef IO io4 __attribute__((ext_vector_type(4)));
+    io4 a;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a[e] = (IO)x[e];
+    u32x2 w;
+    __builtin_memcpy(&w, &a, 8);
+    __builtin_amdgcn_raw_buffer_store_b64(w, r, voff, soff, 0);
+  } else {
+    u32x4 w;
+    __builtin_memcpy(&w, x, 16);
+    __builtin_amdgcn_raw_buffer_store_b128(w, r, voff, soff, 0);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // RoPE.  The packed table is fp32 [(n_pos + 1)][D/2][2] = (cos, sin) per pair;
 // row 0 is the identity (cos 1, sin 0) and serves the CLS token, so token s
 // uses row s + (1 - has_cls) with no branch.
@@ -361,6 +411,14 @@ __device__ __forceinline__ float xor32_pair_op_max(float v) {
 __device__ __forceinline__ float group4_sum(float v) { return xor32_pair_op_sum(xor16_pair_op_sum(v)); }
 __device__ __forceinline__ float group4_max(float v) { return xor32_pair_op_max(xor16_pair_op_max(v)); }
 
+// Work-item / workgroup ids straight from the hardware registers.  (The
+// threadIdx / blockIdx / gridDim accessors are device-library calls, and the
+// kernels here are built with IEEE mode off, which that library is not, so
+// they would not be inlined: every use would become a real call with a stack
+// frame.  The launch grid size is passed in the kernel arguments instead.)
+__device__ __forceinline__ int thread_id() { return __builtin_amdgcn_workitem_id_x(); }
+__device__ __forceinline__ int block_id() { return __builtin_amdgcn_workgroup_id_x(); }
+
 // Workgroups are dispatched round-robin over MI355X's 8 XCDs (each with its
 // own L2).  Remap the linear workgroup id so that XCD x processes one
 // contiguous range of tiles; consecutive tiles (the q/kv blocks of one
@@ -373,5 +431,25 @@ __device__ __forceinline__ int xcd_remap(int L, int T) {
 }
 
 __device__ __forceinline__ int round_up32(int x) { return (x + 31) & ~31; }
+
+// A copy of x the compiler cannot see through.  Index math derived from it is
+// recomputed where it is used instead of being hoisted out of the enclosing
+// loops, which keeps per-lane addresses of rarely run phases (per-plane
+// prologue / epilogue) from occupying registers through the hot loop.
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// Workgroup barrier that orders LDS traffic only.  The waves of these kernels
+// exchange data through LDS alone, so the barrier waits for outstanding LDS
+// operations (lgkmcnt) but not for global loads and stores (vmcnt): prefetches
+// of the next tile and stores of finished results stay in flight across it.
+// (__syncthreads() would drain every outstanding global access first.)
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 }  // namespace farope

@@ -130,7 +130,7 @@ fwd_kernel(const FwdParams p) {
     }
   };
 
-  const int tid = threadIdx.x;
+  const int tid = thread_id();
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (SGPR)
   const int lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
@@ -138,23 +138,23 @@ fwd_kernel(const FwdParams p) {
   // Item of this workgroup at iteration `it` (-1 when done).  Within an
   // iteration, items are dealt XCD-major so neighbouring items (the q blocks
   // of one plane) run on the same XCD and share its L2.
-  const int pos = xcd_remap(blockIdx.x, gridDim.x);
-  auto item_of = [&](int it) {
-    const int item = it * (int)gridDim.x + pos;
+  const int pos = xcd_remap(block_id(), p.n_wg);
+  auto item_of = [&](int it) __attribute__((always_inline)) {
+    const int item = it * p.n_wg + pos;
     return item < p.n_items ? item : -1;
   };
-  auto plane_base = [&](const void* base, const int64_t* st, int plane) {
+  auto plane_base = [&](const void* base, const int64_t* st, int plane) __attribute__((always_inline)) {
     const int bb = plane / p.H, hh = plane - bb * p.H;
     return static_cast<const IO*>(base) + bb * st[0] + hh * st[1];
   };
   // Chunk c of an item starts at key ((c + nch - 1) % nch) * KC: ragged chunk first.
-  auto chunk_start = [&](int c) { return ((c + nch - 1) % nch) * KC; };
+  auto chunk_start = [&](int c) __attribute__((always_inline)) { return ((c + nch - 1) % nch) * KC; };
 
   // ---- KV chunk prefetch registers: two rows x 8 channels of K and V
   //      (+ their cos/sin when the table is not in LDS) ----
   Raw8<IO> pk[ITER][2], pv[ITER][2];
   float pcs[ITER][2][kTabLds ? 1 : 8];
-  auto prefetch_kv = [&](int item, int c) {
+  auto prefetch_kv = [&](int item, int c) __attribute__((always_inline)) {
     const int plane = item / p.n_blk;
     const IO* __restrict__ K = plane_base(p.k, p.sk, plane);
     const IO* __restrict__ V = plane_base(p.v, p.sv, plane);
@@ -181,7 +181,7 @@ fwd_kernel(const FwdParams p) {
       }
     }
   };
-  auto commit_kv = [&](int slot, int kvb) {
+  auto commit_kv = [&](int slot, int kvb) __attribute__((always_inline)) {
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
       const int u = tid + it * NT;
@@ -213,7 +213,7 @@ fwd_kernel(const FwdParams p) {
   // ---- Q rows of an item: raw prefetch registers -> rotated B-operand fragments ----
   Raw8<IO> qraw[QT][KS];
   float qcs[QT][KS][kTabLds ? 1 : 8];
-  auto prefetch_q = [&](int item) {
+  auto prefetch_q = [&](int item) __attribute__((always_inline)) {
     const int plane = item / p.n_blk, qb = item - plane * p.n_blk;
     const IO* __restrict__ Q = plane_base(p.q, p.sq, plane);
 #pragma unroll
@@ -236,7 +236,7 @@ fwd_kernel(const FwdParams p) {
     }
   };
   Frag qf[QT][KS];
-  auto commit_q = [&](int qb) {
+  auto commit_q = [&](int qb) __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < QT; ++t)
 #pragma unroll
@@ -269,7 +269,7 @@ fwd_kernel(const FwdParams p) {
   // guards, and for the 16-row-ragged N of ViT planes the extra work lands on
   // SIMDs that would otherwise wait at the next barrier.  MASKED: the block
   // holding key N-1 (keys >= N get probability 0).
-  auto block = [&](auto maskc, const S* __restrict__ cK, const S* __restrict__ cV, int kvb, int j) {
+  auto block = [&](auto maskc, const S* __restrict__ cK, const S* __restrict__ cV, int kvb, int j) __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(maskc)::value;
     // ---- S^T = K-hat Q-hat^T for 32 keys (each K-hat fragment feeds QT MFMAs) ----
     f32x4 sacc[QT][2];
@@ -326,7 +326,7 @@ fwd_kernel(const FwdParams p) {
     }
   };
   // One KV chunk: full blocks, then the block holding key N-1 if it is ragged.
-  auto chunk = [&](const S* __restrict__ cK, const S* __restrict__ cV, int kvb) {
+  auto chunk = [&](const S* __restrict__ cK, const S* __restrict__ cV, int kvb) __attribute__((always_inline)) {
     const int nkeys = min(KC, N - kvb);
     const int nfull = nkeys / 32;
     for (int j = 0; j < nfull; ++j) block(std::false_type{}, cK, cV, kvb, j);
@@ -346,7 +346,7 @@ fwd_kernel(const FwdParams p) {
       const int r = i / V4, c = i - r * V4;
       *reinterpret_cast<f32x4*>(&sTab[r * TP + 4 * c]) = src[i];
     }
-    __syncthreads();
+    lds_barrier();
   }
   int g = 0;   // chunks consumed so far: LDS slot g & 1
   while (item >= 0) {
@@ -372,7 +372,7 @@ fwd_kernel(const FwdParams p) {
         prefetch_kv(nxt, 0);
       }
       if (c == 0 && nxt >= 0) prefetch_q(nxt);
-      __syncthreads();
+      lds_barrier();
       if (nt > 0) chunk(sK[slot], sVt[slot], chunk_start(c));
     }
 
@@ -415,8 +415,9 @@ int fwd_block_rows(int D) {
 int fwd_threads(int D) { return D == 64 ? FwdShape<64>::NW * 64 : FwdShape<128>::NW * 64; }
 
 template <typename IO, int CT, int D>
-static hipError_t fwd_launch(const FwdParams& p, hipStream_t st) {
+static hipError_t fwd_launch(const FwdParams& p0, hipStream_t st) {
   using SH = FwdShape<D>;
+  FwdParams p = p0;
   // fp32 compute keeps 4-byte tiles in LDS: no room for the table copy there
   constexpr int TR = CT == DT_F32 ? 0 : SH::TABROWS;
   const bool tab = TR > 0 && p.N + 1 - p.has_cls <= TR;
@@ -427,6 +428,7 @@ static hipError_t fwd_launch(const FwdParams& p, hipStream_t st) {
                          : fwd_kernel<IO, CT, D, SH::NW, SH::QT, SH::KC, 0, false>);
   const int grid = persistent_grid(reinterpret_cast<const void*>(kern), SH::NW * 64, p.n_items);
   if (grid <= 0) return hipErrorInvalidConfiguration;
+  p.n_wg = grid;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(SH::NW * 64), 0, st, p);
   return hipGetLastError();
 }

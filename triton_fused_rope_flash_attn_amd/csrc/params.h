@@ -22,6 +22,7 @@ struct FwdParams {
   int vec_q, vec_k, vec_v, vec_o;
   int n_blk;           // q blocks per plane
   int n_items;         // planes * n_blk work items
+  int n_wg;            // workgroups of the launch (set by the launcher)
 };
 
 struct BwdParams {
@@ -42,6 +43,7 @@ struct BwdParams {
   float scale_log2;    // softmax_scale * log2(e)
   int vec_q, vec_k, vec_v, vec_o, vec_do, vec_dq, vec_dk, vec_dv;
   int n_blk;           // q blocks (dq kernel) or kv blocks (dk/dv kernel) per plane
+  int n_wg;            // workgroups of the launch (set by the launcher)
 };
 
 // Launch shapes picked by the tile table (api.hip).
@@ -62,8 +64,9 @@ hipError_t launch_rope_pack(const float* cosp, int64_t cs0, int64_t cs1, const f
                             int64_t ss0, int64_t ss1, int n_pos, int d2, float* out,
                             hipStream_t st);
 
-// Workgroups for a persistent kernel: min(items, CUs x resident workgroups per CU).
-int persistent_grid(const void* kernel, int block_threads, int items);
+// Workgroups for a persistent kernel: min(items, CUs x resident workgroups per
+// CU), with `dyn_lds` bytes of dynamic LDS per workgroup; <= 0 on a HIP error.
+int persistent_grid(const void* kernel, int block_threads, int items, size_t dyn_lds = 0);
 
 // Rows of q (fwd, dq) or kv (dk/dv) one work item / workgroup covers.
 int fwd_block_rows(int D);
