@@ -101,11 +101,17 @@ fwd_kernel(const FwdParams p) {
   // TABROWS == 0: rotations read the table from global memory (L2-resident).
   constexpr bool kTabLds = TABROWS > 0;
 
+  // 16-bit compute: V is kept row-major (raw rows when IO is the compute
+  // type) and V^T fragments are read transposed (ds_read_b64_tr_b16); fp32
+  // compute keeps an explicitly transposed V^T tile.
+  constexpr bool TRV = sizeof(S) == 2;
   __shared__ __attribute__((aligned(16))) S sK[2][KC * LDK];
-  __shared__ __attribute__((aligned(16))) S sVt[2][D * LDV];
-  // LDS copy of the packed table: row pitch D + 4 floats (bank-spread rows).
-  constexpr int TP = D + 4;
-  __shared__ __attribute__((aligned(16))) float sTab[kTabLds ? TABROWS * TP : 4];
+  __shared__ __attribute__((aligned(16))) S sVt[2][TRV ? KC * LDK : D * LDV];
+  // LDS copy of the packed table: D/2 (cos, sin) pairs = D floats per row,
+  // 16-byte chunk c of row r stored at chunk c ^ (r & (D/4 - 1)) (bank-spread
+  // without padding).
+  constexpr int TCH = D / 4;          // 16-byte chunks per table row (D floats)
+  __shared__ __attribute__((aligned(16))) float sTab[kTabLds ? TABROWS * 2 * D / 2 : 4];
 
   const int N = p.N;
   const int nch = (N + KC - 1) / KC;  // KV chunks per item
@@ -116,14 +122,15 @@ fwd_kernel(const FwdParams p) {
   // cos/sin of pairs p0 .. p0+3 of table row `row`.  `swap` lanes fetch the
   // two 16-byte halves in the opposite order (spreads banks when neighbouring
   // lanes read the same columns of two rows).
-  auto tab4 = [&](int row, int p0, float (&cs)[8], int swap) {
+  auto tab4 = [&](int row, int p0, float (&cs)[8]) __attribute__((always_inline)) {
     if constexpr (kTabLds) {
-      const f32x4* t = reinterpret_cast<const f32x4*>(&sTab[row * TP + 2 * p0]);
-      const f32x4 a = t[swap], b = t[swap ^ 1];
+      const int c = p0 >> 1;   // chunks c, c + 1 hold pairs p0 .. p0+3
+      const f32x4 a = *reinterpret_cast<const f32x4*>(&sTab[(row * TCH + (c ^ (row & (TCH - 1)))) * 4]);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(&sTab[(row * TCH + ((c + 1) ^ (row & (TCH - 1)))) * 4]);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        cs[e] = swap ? b[e] : a[e];
-        cs[4 + e] = swap ? a[e] : b[e];
+        cs[e] = a[e];
+        cs[4 + e] = b[e];
       }
     } else {
       rope_load4(p.rope, row, D2, p0, cs);
@@ -195,17 +202,30 @@ fwd_kernel(const FwdParams p) {
           if constexpr (kTabLds) {
             // rows past N hold zeros; any in-table row serves for them
             float cs[8];
-            tab4(min(kvb + 2 * rp + x, N - 1) + shift, 4 * cc, cs, rp & 1);
+            tab4(min(kvb + 2 * rp + x, N - 1) + shift, 4 * cc, cs);
             rope_rotate8(xk, cs);
           } else {
             rope_rotate8(xk, pcs[it][x]);
           }
           C::put8(&sK[slot][kperm(2 * rp + x) * LDK + 8 * cc], xk);
-          unpack8(pv[it][x], xv[x]);
+          if constexpr (TRV) {
+            S* dst = &sVt[slot][(2 * rp + x) * LDK + 8 * cc];
+            if constexpr (std::is_same<IO, S>::value) {
+              *reinterpret_cast<typename Raw8<IO>::vec*>(dst) = pv[it][x].v;   // raw row segment
+            } else {
+              float y[8];
+              unpack8(pv[it][x], y);
+              C::put8(dst, y);
+            }
+          } else {
+            unpack8(pv[it][x], xv[x]);
+          }
         }
+        if constexpr (!TRV) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          put2<CT>(&sVt[slot][(8 * cc + e) * LDV + vswz(8 * cc + e, 2 * rp)], xv[0][e], xv[1][e]);
+          for (int e = 0; e < 8; ++e)
+            put2<CT>(&sVt[slot][(8 * cc + e) * LDV + vswz(8 * cc + e, 2 * rp)], xv[0][e], xv[1][e]);
+        }
       }
     }
   };
@@ -246,7 +266,7 @@ fwd_kernel(const FwdParams p) {
         if constexpr (kTabLds) {
           const int row = (qb * NW * QT + t * NW + wave) * 16 + lr;
           float cs[8];
-          tab4(min(row, N - 1) + shift, 16 * s + 4 * lg, cs, 0);
+          tab4(min(row, N - 1) + shift, 16 * s + 4 * lg, cs);
           rope_rotate8(x, cs);
         } else {
           rope_rotate8(x, qcs[t][s]);
@@ -320,7 +340,12 @@ fwd_kernel(const FwdParams p) {
     // ---- O^T += V^T P^T (each V^T fragment feeds QT MFMAs) ----
 #pragma unroll
     for (int d = 0; d < DT; ++d) {
-      const Frag a = C::lds(&cV[(16 * d + lr) * LDV + vswz(16 * d + lr, 32 * j + 8 * lg)]);
+      // A = V^T rows 16d.., k-slot e <-> key 32j + 8lg + e (the P^T order)
+      Frag a;
+      if constexpr (TRV)
+        a = C::tr(cV + tr_offset(32 * j + 8 * lg, 16 * d, LDK, lr), cV + tr_offset(32 * j + 8 * lg + 4, 16 * d, LDK, lr));
+      else
+        a = C::lds(&cV[(16 * d + lr) * LDV + vswz(16 * d + lr, 32 * j + 8 * lg)]);
 #pragma unroll
       for (int t = 0; t < QT; ++t) oacc[t][d] = C::mma(a, pf[t], oacc[t][d]);
     }
@@ -339,12 +364,11 @@ fwd_kernel(const FwdParams p) {
   prefetch_kv(item, 0);
   prefetch_q(item);
   if constexpr (kTabLds) {
-    // rows 0 .. N-1+shift of the packed table, D floats each -> pitch TP
-    constexpr int V4 = D / 4;   // f32x4 per row
+    // rows 0 .. N-1+shift of the packed table (TCH 16-byte chunks each), swizzled
     const f32x4* src = reinterpret_cast<const f32x4*>(p.rope);
-    for (int i = tid; i < (N + shift) * V4; i += NT) {
-      const int r = i / V4, c = i - r * V4;
-      *reinterpret_cast<f32x4*>(&sTab[r * TP + 4 * c]) = src[i];
+    for (int i = tid; i < (N + shift) * TCH; i += NT) {
+      const int r = i / TCH, c = i - r * TCH;
+      *reinterpret_cast<f32x4*>(&sTab[(r * TCH + (c ^ (r & (TCH - 1)))) * 4]) = src[i];
     }
     lds_barrier();
   }
