@@ -144,10 +144,13 @@ bwd_plane_kernel(const BwdParams p) {
         pq = pg = po = zero_raw8<IO>();
       }
     }
+    // raw LSE (scaled and masked at commit, so no wait is forced here: a
+    // wait on this load would also drain the Q / dO / O loads issued above);
+    // the buffer range is the plane's N values, rows >= N read 0
     const int lt = tid - 256;
     if (lt >= 0 && lt < QS) {
-      const float* l = p.lse + (int64_t)plane * N + qb;
-      plse = qb + lt < N ? l[lt] * kLog2e : INFINITY;
+      const auto rl = make_rsrc(p.lse + (int64_t)plane * N, (unsigned)N * 4u);
+      plse = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rl, (unsigned)lt * 4u, (unsigned)qb * 4u, 0));
     }
   };
   auto commit = [&](int buf, int qb) __attribute__((always_inline)) {
@@ -173,7 +176,7 @@ bwd_plane_kernel(const BwdParams p) {
       d += __shfl_xor(d, 4);
       if (sc == 0) sDl[buf][sr] = d;
     } else if (t - 256 < QS) {
-      sL2[buf][t - 256] = plse;
+      sL2[buf][t - 256] = qb + (t - 256) < N ? plse * kLog2e : INFINITY;
     }
   };
 
@@ -236,6 +239,10 @@ bwd_plane_kernel(const BwdParams p) {
         rope_rotate8(x, cs);
         kf[u][s] = C::make(x);
         vf[u][s] = C::make(y);
+        // materialise V here (for 16-bit I/O the conversion folds away and the
+        // fragment would alias the load registers, moving the wait for these
+        // loads into the first sweep, behind the next stage's prefetch)
+        asm volatile("" : "+v"(vf[u][s].v));
         *reinterpret_cast<decltype(kf[u][s].v)*>(&sK[(kw + 16 * u + lr) * LD + 32 * s + 8 * lg]) =
             kf[u][s].v;
       }
@@ -412,12 +419,12 @@ bwd_plane_kernel(const BwdParams p) {
       if (st > 0) commit(buf, qb);
       lds_barrier();
       // next stage, or the next plane's first stage (the last plane re-reads its
-      // own first stage: unconditional loads keep these registers' live
-      // ranges inside one loop iteration)
-      if (st + 1 < nstages) {
-        prefetch(plane, qb + QS);
-      } else {
-        prefetch(nxt >= 0 ? nxt : plane, 0);
+      // own first stage).  One unconditional call with a uniformly selected
+      // target: the loads land directly in the staging registers, with no
+      // merge copies that would force an early wait on them.
+      {
+        const bool last = st + 1 == nstages;
+        prefetch(last ? (nxt >= 0 ? nxt : plane) : plane, last ? 0 : qb + QS);
       }
       if (st > 0) dq(plane, st - 1);
       if (nu == 2) {

@@ -157,12 +157,40 @@ fwd_kernel(const FwdParams p) {
   // Chunk c of an item starts at key ((c + nch - 1) % nch) * KC: ragged chunk first.
   auto chunk_start = [&](int c) __attribute__((always_inline)) { return ((c + nch - 1) % nch) * KC; };
 
+  // VEC: the host guarantees unit d-stride, 16-byte alignment and in-plane
+  // byte offsets below 2^31.  Prefetches then go through buffer descriptors
+  // over rows 0 .. N-1 of the plane: unconditional (rows >= N read 0), with
+  // 32-bit lane byte offsets, so the wait-count pass can track each prefetch
+  // precisely instead of draining all outstanding loads at control-flow joins.
+  constexpr unsigned ES = sizeof(IO);
+  auto rsrc = [&](const void* b, const int64_t* st, int plane) __attribute__((always_inline)) {
+    return make_rsrc(plane_base(b, st, plane), (unsigned)(((int64_t)(N - 1) * st[2] + D) * ES));
+  };
+
   // ---- KV chunk prefetch registers: two rows x 8 channels of K and V
   //      (+ their cos/sin when the table is not in LDS) ----
   Raw8<IO> pk[ITER][2], pv[ITER][2];
   float pcs[ITER][2][kTabLds ? 1 : 8];
   auto prefetch_kv = [&](int item, int c) __attribute__((always_inline)) {
     const int plane = item / p.n_blk;
+    if constexpr (VEC && kTabLds && UNITS % NT == 0) {
+      const int kvb = chunk_start(c);
+      const auto rK = rsrc(p.k, p.sk, plane), rV = rsrc(p.v, p.sv, plane);
+#pragma unroll
+      for (int it = 0; it < ITER; ++it) {
+        const int u = tid + it * NT;
+        const int rp = u / CPR, cc = u - rp * CPR;
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+          const int r = 2 * rp + x;
+          pk[it][x] = buf_load8<IO>(rK, (unsigned)((r * (int)p.sk[2] + 8 * cc) * (int)ES),
+                                    (unsigned)(kvb * (int)p.sk[2] * (int)ES));
+          pv[it][x] = buf_load8<IO>(rV, (unsigned)((r * (int)p.sv[2] + 8 * cc) * (int)ES),
+                                    (unsigned)(kvb * (int)p.sv[2] * (int)ES));
+        }
+      }
+      return;
+    }
     const IO* __restrict__ K = plane_base(p.k, p.sk, plane);
     const IO* __restrict__ V = plane_base(p.v, p.sv, plane);
     const int kvb = chunk_start(c);
@@ -235,6 +263,17 @@ fwd_kernel(const FwdParams p) {
   float qcs[QT][KS][kTabLds ? 1 : 8];
   auto prefetch_q = [&](int item) __attribute__((always_inline)) {
     const int plane = item / p.n_blk, qb = item - plane * p.n_blk;
+    if constexpr (VEC && kTabLds) {
+      const auto rQ = rsrc(p.q, p.sq, plane);
+#pragma unroll
+      for (int t = 0; t < QT; ++t) {
+        const int row = (qb * NW * QT + t * NW + wave) * 16 + lr;
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+          qraw[t][s] = buf_load8<IO>(rQ, (unsigned)((row * (int)p.sq[2] + 32 * s + 8 * lg) * (int)ES), 0u);
+      }
+      return;
+    }
     const IO* __restrict__ Q = plane_base(p.q, p.sq, plane);
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
@@ -387,18 +426,24 @@ fwd_kernel(const FwdParams p) {
       for (int d = 0; d < DT; ++d) oacc[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    for (int c = 0; c < nch; ++c, ++g) {
+    // One KV chunk: stage it into LDS, start the next chunk (or the next
+    // item's first chunk) with one call on a uniformly selected target, and --
+    // after the first chunk is staged -- the next item's Q rows (the last item
+    // re-reads its own).  Unconditional loads with no merge copies let every
+    // wait cover exactly the load it needs.
+    auto chunk_step = [&](auto firstc, int c) __attribute__((always_inline)) {
+      constexpr bool FIRST = decltype(firstc)::value;
       const int slot = g & 1;
       commit_kv(slot, chunk_start(c));
-      if (c + 1 < nch) {
-        prefetch_kv(item, c + 1);
-      } else if (nxt >= 0) {
-        prefetch_kv(nxt, 0);
-      }
-      if (c == 0 && nxt >= 0) prefetch_q(nxt);
+      const bool last = c + 1 == nch;
+      prefetch_kv(last ? (nxt >= 0 ? nxt : item) : item, last ? 0 : c + 1);
+      if constexpr (FIRST) prefetch_q(nxt >= 0 ? nxt : item);
       lds_barrier();
       if (nt > 0) chunk(sK[slot], sVt[slot], chunk_start(c));
-    }
+      ++g;
+    };
+    chunk_step(std::true_type{}, 0);
+    for (int c = 1; c < nch; ++c) chunk_step(std::false_type{}, c);
 
     // ---- epilogue: lane holds O[row][16d + 4lg + (0..3)] ----
     IO* __restrict__ O = const_cast<IO*>(plane_base(p.o, p.so, plane));
