@@ -40,9 +40,26 @@ namespace {
 constexpr int kPlaneNW = 8;                   // waves per workgroup
 constexpr int kPlaneQS = 32;                  // query rows per stage
 constexpr int kPlaneMaxN = kPlaneNW * 32;     // keys per workgroup
-constexpr int kPlaneLD = 64 + 8;              // pitch of the Q-hat / dO / K-hat tiles (elements)
-constexpr int kPlaneLDD = kPlaneQS + 8;       // pitch of the key-major dS^T tile (elements)
+constexpr int kPlaneLD = 64;                  // pitch of the Q-hat / dO / K-hat tiles (elements)
+constexpr int kPlaneLDD = kPlaneQS;           // pitch of the key-major dS^T tile (elements)
 }  // namespace
+
+// Unpadded LDS tiles with their 16-byte chunks XOR-swizzled per row.  The
+// swizzles are chosen (and checked against a 64-bank model) so that every
+// access pattern of the kernel is conflict-free: 16-byte reads of 16
+// consecutive rows, transposed 8-byte reads of rows {4lg + e} and
+// {8lg + e, 8lg + 4 + e}, 16-byte row writes and 8-byte dS^T writes.  Both
+// have period 16 in the row, so row offsets by multiples of 16 stay
+// compile-time constants.
+// Q-hat / dO / K-hat: 128-byte rows (8 chunks).
+__device__ __forceinline__ int sw64(int r, int col) {
+  const int f = ((((r >> 1) & 3) ^ ((r >> 2) & 2)) << 1) | ((r >> 3) & 1);
+  return r * 64 + ((((col >> 3) ^ f)) << 3) + (col & 7);
+}
+// dS^T: 64-byte rows (4 chunks).
+__device__ __forceinline__ int sw32(int r, int col) {
+  return r * 32 + ((((col >> 3) ^ ((r >> 2) & 3))) << 3) + (col & 7);
+}
 
 // LDS copy of the RoPE table rows a plane uses, one 256-byte row (32 pairs of
 // (cos, sin)) per token.  The sixteen 16-byte chunks of token row r are
@@ -165,8 +182,8 @@ bwd_plane_kernel(const BwdParams p) {
       const f32x4 c0 = tab_chunk(sTab, row, 2 * sc), c1 = tab_chunk(sTab, row, 2 * sc + 1);
       const float cs[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
       rope_rotate8(x, cs);
-      C::put8(&sQ[buf][sr * LD + 8 * sc], x);
-      C::put8(&sG[buf][sr * LD + 8 * sc], g);
+      C::put8(&sQ[buf][sw64(sr, 8 * sc)], x);
+      C::put8(&sG[buf][sw64(sr, 8 * sc)], g);
       // delta = rowsum(dO * O); the 8 chunks of a row are 8 consecutive lanes
       float d = 0.f;
 #pragma unroll
@@ -243,7 +260,7 @@ bwd_plane_kernel(const BwdParams p) {
         // fragment would alias the load registers, moving the wait for these
         // loads into the first sweep, behind the next stage's prefetch)
         asm volatile("" : "+v"(vf[u][s].v));
-        *reinterpret_cast<decltype(kf[u][s].v)*>(&sK[(kw + 16 * u + lr) * LD + 32 * s + 8 * lg]) =
+        *reinterpret_cast<decltype(kf[u][s].v)*>(&sK[sw64(kw + 16 * u + lr, 32 * s + 8 * lg)]) =
             kf[u][s].v;
       }
     }
@@ -271,15 +288,19 @@ bwd_plane_kernel(const BwdParams p) {
     const int buf = sp & 1;
     const int qb = sp * QS;
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    // lane parts of the transposed-read offsets (rows 8lg + lr/4); the key
-    // block adds a compile-time constant (folded into the instruction)
-    const S* ka = &sK[tr_offset(8 * lg, 16 * dd, LD, lr)];
-    const S* db = &sdS[buf][tr_offset(8 * lg, 16 * qt, LDD, lr)];
+    // lane parts of the transposed-read offsets (rows 8lg + lr/4 and
+    // 8lg + 4 + lr/4, column 4(lr%4) of the slice); the key block adds a
+    // compile-time constant (the swizzles have period 16 in the row)
+    const int r0 = 8 * lg + (lr >> 2);
+    const S* ka0 = &sK[sw64(r0, 16 * dd + 4 * (lr & 3))];
+    const S* ka1 = &sK[sw64(r0 + 4, 16 * dd + 4 * (lr & 3))];
+    const S* db0 = &sdS[buf][sw32(r0, 16 * qt + 4 * (lr & 3))];
+    const S* db1 = &sdS[buf][sw32(r0 + 4, 16 * qt + 4 * (lr & 3))];
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
       // A = K-hat^T rows 16dd.., B = dS^T columns 16qt..; k = keys 32kb + 8lg + (0..7)
-      const Frag a = C::tr(ka + 32 * kb * LD, ka + (32 * kb + 4) * LD);
-      const Frag b = C::tr(db + 32 * kb * LDD, db + (32 * kb + 4) * LDD);
+      const Frag a = C::tr(ka0 + 32 * kb * LD, ka1 + 32 * kb * LD);
+      const Frag b = C::tr(db0 + 32 * kb * LDD, db1 + 32 * kb * LDD);
       acc = C::mma(a, b, acc);
     }
     const int row = qb + 16 * qt + lr;
@@ -339,8 +360,8 @@ bwd_plane_kernel(const BwdParams p) {
         const int qr = 16 * h + lr;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          const Frag a = C::lds(q + qr * LD + 32 * s + 8 * lg);
-          const Frag b = C::lds(g + qr * LD + 32 * s + 8 * lg);
+          const Frag a = C::lds(q + sw64(qr, 32 * s + 8 * lg));
+          const Frag b = C::lds(g + sw64(qr, 32 * s + 8 * lg));
 #pragma unroll
           for (int u = 0; u < NUA; ++u) {
             sacc[u] = C::mma(a, kf[u][s], sacc[u]);
@@ -358,14 +379,14 @@ bwd_plane_kernel(const BwdParams p) {
           C::set2(pf[u], 2 * h + 1, pv[2], pv[3]);
           C::set2(dsf[u], 2 * h, dsv[0], dsv[1]);
           C::set2(dsf[u], 2 * h + 1, dsv[2], dsv[3]);
-          C::put4(ds + (kw + 16 * u + lr) * LDD + q0, dsf[u], h);
+          C::put4(ds + sw32(kw + 16 * u + lr, q0), dsf[u], h);
         }
       }
       // dV^T += dO^T P ; dK-hat^T += Q-hat^T dS  (k = queries 16h + 4lg + e)
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
-        const int o0 = tr_offset(4 * lg, 0, LD, lr) + 16 * d;   // rows 4lg + e
-        const int o1 = o0 + 16 * LD;                            // rows 16 + 4lg + e
+        const int o0 = sw64(4 * lg + (lr >> 2), 16 * d + 4 * (lr & 3));   // rows 4lg + e
+        const int o1 = o0 + 16 * LD;                                      // rows 16 + 4lg + e
         const Frag ag = C::tr(g + o0, g + o1);
         const Frag aq = C::tr(q + o0, q + o1);
 #pragma unroll
@@ -381,8 +402,8 @@ bwd_plane_kernel(const BwdParams p) {
       const int kv0 = kw + 16 * u;
       if (kv0 < nkv32) {
         const Frag z = C::zero();
-        C::put4(ds + (kv0 + lr) * LDD + 4 * lg, z, 0);
-        C::put4(ds + (kv0 + lr) * LDD + 16 + 4 * lg, z, 0);
+        C::put4(ds + sw32(kv0 + lr, 4 * lg), z, 0);
+        C::put4(ds + sw32(kv0 + lr, 16 + 4 * lg), z, 0);
       }
     }
   };

@@ -314,7 +314,7 @@ fwd_kernel(const FwdParams p) {
       }
   };
 
-  float m_run[QT], l_run[QT];
+  float m_run[QT], l_run[QT], m_thr[QT];
   f32x4 oacc[QT][DT];
 
   // One KV chunk for all QT subtiles of the wave.  Subtiles past the last
@@ -357,16 +357,20 @@ fwd_kernel(const FwdParams p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) sv[e] = e < lim ? sv[e] : -INFINITY;
       }
-      float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                       fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-      mx = group4_max(mx) * c2;
-      if (__any(mx > m_run[t] + kRescaleSlack)) {
+      // The running max only has to bound the exponent: rescale (group max,
+      // O and row sum times 2^(m_old - m_new)) only when some lane's own max
+      // exceeds m_run + slack; m_thr = (m_run + slack) / c2 in logit units.
+      const float ml = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                             fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+      if (__any(ml > m_thr[t])) {
+        const float mx = group4_max(ml) * c2;
         const float mnew = fmaxf(m_run[t], mx);
         const float alpha = fast_exp2(m_run[t] - mnew);
         l_run[t] *= alpha;
 #pragma unroll
         for (int d = 0; d < DT; ++d) oacc[t][d] *= alpha;
         m_run[t] = mnew;
+        m_thr[t] = (mnew + kRescaleSlack) / c2;
       }
       float pv8[8];
 #pragma unroll
@@ -421,6 +425,7 @@ fwd_kernel(const FwdParams p) {
     for (int t = 0; t < QT; ++t) {
       nt += (qb * NW * QT + t * NW + wave) * 16 < N;
       m_run[t] = -INFINITY;
+      m_thr[t] = -INFINITY;
       l_run[t] = 0.f;
 #pragma unroll
       for (int d = 0; d < DT; ++d) oacc[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
