@@ -72,7 +72,10 @@ __device__ __forceinline__ f32x4 tab_chunk(const float* t, int row, int c) {
 
 // VEC: every tensor of the call allows 16-byte vector access (decided on the
 // host); the generic instantiation gathers element by element instead.
-template <typename IO, int CT, bool VEC>
+// NKB: 32-key blocks summed by the dQ products, 8 or (for N = 193 .. 224, the
+// ViT-S/B planes) 7; dS^T rows and K-hat rows of keys >= N are zero, so
+// blocks beyond the plane's keys add nothing.
+template <typename IO, int CT, bool VEC, int NKB>
 __global__ void __launch_bounds__(kPlaneNW * 64)
 bwd_plane_kernel(const BwdParams p) {
   using C = Comp<CT>;
@@ -101,7 +104,6 @@ bwd_plane_kernel(const BwdParams p) {
   const int lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
   const int nkv32 = round_up32(N);
-  const int nkb = nkv32 >> 5;                                  // 32-key blocks
   const int nstages = (N + QS - 1) / QS;
   const int kw = 32 * wave;                                    // first key of this wave
   const int nu = (kw < N) + (kw + 16 < N);                     // active 16-key subtiles
@@ -188,9 +190,7 @@ bwd_plane_kernel(const BwdParams p) {
       float d = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) d += g[e] * o[e];
-      d += __shfl_xor(d, 1);
-      d += __shfl_xor(d, 2);
-      d += __shfl_xor(d, 4);
+      d = dpp_sum8(d);
       if (sc == 0) sDl[buf][sr] = d;
     } else if (t - 256 < QS) {
       sL2[buf][t - 256] = qb + (t - 256) < N ? plse * kLog2e : INFINITY;
@@ -277,31 +277,52 @@ bwd_plane_kernel(const BwdParams p) {
 
   f32x4 dvacc[2][4], dkacc[2][4];
 
+  // A-operands of this wave's dQ tile, K-hat^T rows 16dd .. 16dd+15 of every
+  // 32-key block (k = keys 32kb + 8lg + (0..7)), read transposed from sK.
+  // Lane parts of the read offsets are rows 8lg + lr/4 and 8lg + 4 + lr/4,
+  // column 4(lr%4) of the slice; the key block adds a compile-time constant
+  // (the swizzles have period 16 in the row).  Rows of keys >= N are zero.
+  // With 16-bit I/O they are read once per plane and kept in registers for
+  // all of its stages; 32-bit I/O needs those registers for its staging and
+  // reads them per stage.
+  constexpr bool KQREG = sizeof(IO) == 2;
+  Frag kq[KQREG ? NKB : 1];
+  auto ka_tr = [&](int kb) __attribute__((always_inline)) {
+    const int lane = opaque(tid & 63), lr = lane & 15, lg = lane >> 4;
+    const int r0 = 8 * lg + (lr >> 2);
+    const S* ka0 = &sK[sw64(r0, 16 * dd + 4 * (lr & 3))];
+    const S* ka1 = &sK[sw64(r0 + 4, 16 * dd + 4 * (lr & 3))];
+    return C::tr(ka0 + 32 * kb * LD, ka1 + 32 * kb * LD);
+  };
+  auto load_kq = [&]() __attribute__((always_inline)) {
+    if constexpr (KQREG) {
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) kq[kb] = ka_tr(kb);
+    }
+  };
+
   // ---- dQ of one finished stage from its dS^T tile: this wave's 16x16 tile
   //      dQ-hat^T[16dd.., 16qt..] = K-hat^T dS^T, un-rotated and stored.
   //      NKB = number of 32-key blocks (straight-line code, no per-block branch) ----
   // VEC lane byte offset of this lane's dQ element (row 16qt + lr of a stage, channel 16dd + 4lg)
   const unsigned bdq = VEC ? boff(p.sdq, 16 * qt + lr, 16 * dd + 4 * lg) : 0u;
-  auto dq_stage = [&](auto nkbc, int plane, int sp) __attribute__((always_inline)) {
-    constexpr int NKB = decltype(nkbc)::value;
+  auto dq = [&](int plane, int sp) __attribute__((always_inline)) {
     const int lane = opaque(tid & 63), lr = lane & 15, lg = lane >> 4;
     const int buf = sp & 1;
     const int qb = sp * QS;
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    // lane parts of the transposed-read offsets (rows 8lg + lr/4 and
-    // 8lg + 4 + lr/4, column 4(lr%4) of the slice); the key block adds a
-    // compile-time constant (the swizzles have period 16 in the row)
+    // lane parts of the transposed-read offsets as for kq
     const int r0 = 8 * lg + (lr >> 2);
-    const S* ka0 = &sK[sw64(r0, 16 * dd + 4 * (lr & 3))];
-    const S* ka1 = &sK[sw64(r0 + 4, 16 * dd + 4 * (lr & 3))];
     const S* db0 = &sdS[buf][sw32(r0, 16 * qt + 4 * (lr & 3))];
     const S* db1 = &sdS[buf][sw32(r0 + 4, 16 * qt + 4 * (lr & 3))];
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
       // A = K-hat^T rows 16dd.., B = dS^T columns 16qt..; k = keys 32kb + 8lg + (0..7)
-      const Frag a = C::tr(ka0 + 32 * kb * LD, ka1 + 32 * kb * LD);
       const Frag b = C::tr(db0 + 32 * kb * LDD, db1 + 32 * kb * LDD);
-      acc = C::mma(a, b, acc);
+      if constexpr (KQREG)
+        acc = C::mma(kq[kb], b, acc);
+      else
+        acc = C::mma(ka_tr(kb), b, acc);
     }
     const int row = qb + 16 * qt + lr;
     if (row < N) {
@@ -322,19 +343,6 @@ bwd_plane_kernel(const BwdParams p) {
       }
     }
   };
-  auto dq = [&](int plane, int sp) __attribute__((always_inline)) {
-    switch (nkb) {
-      case 1: dq_stage(std::integral_constant<int, 1>{}, plane, sp); break;
-      case 2: dq_stage(std::integral_constant<int, 2>{}, plane, sp); break;
-      case 3: dq_stage(std::integral_constant<int, 3>{}, plane, sp); break;
-      case 4: dq_stage(std::integral_constant<int, 4>{}, plane, sp); break;
-      case 5: dq_stage(std::integral_constant<int, 5>{}, plane, sp); break;
-      case 6: dq_stage(std::integral_constant<int, 6>{}, plane, sp); break;
-      case 7: dq_stage(std::integral_constant<int, 7>{}, plane, sp); break;
-      default: dq_stage(std::integral_constant<int, 8>{}, plane, sp); break;
-    }
-  };
-
   // ---- S, dP, P, dS, dV, dK for the wave's first NUA subtiles over one
   //      32-query stage (query rows in natural order, see above) ----
   auto sweep_keys = [&](auto nuc, int buf) __attribute__((always_inline)) {
@@ -421,6 +429,11 @@ bwd_plane_kernel(const BwdParams p) {
       const int r = i >> 4, c = i & 15;
       *reinterpret_cast<f32x4*>(&sTab[((r << 4) + (c ^ (r & 15))) * 4]) = src[i];
     }
+    // dS^T rows of keys >= round_up32(N) enter the dQ products but are never
+    // written by a sweep: zero them once, in both buffers
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+      for (int i = nkv32 * LDD + tid; i < kPlaneMaxN * LDD; i += kPlaneNW * 64) sdS[b][i] = S(0.f);
   }
   while (plane >= 0) {
     const int nxt = item_of(it + 1);
@@ -429,6 +442,9 @@ bwd_plane_kernel(const BwdParams p) {
     lds_barrier();
     commit_kv();
     commit(0, 0);
+    // sK is complete: this wave's dQ operands
+    lds_barrier();
+    load_kq();
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
@@ -510,7 +526,9 @@ static hipError_t fused_launch(const BwdParams& p0, hipStream_t st) {
   BwdParams p = p0;
   const bool vec = p.vec_q && p.vec_k && p.vec_v && p.vec_o && p.vec_do && p.vec_dq && p.vec_dk &&
                    p.vec_dv;
-  auto kern = vec ? bwd_plane_kernel<IO, CT, true> : bwd_plane_kernel<IO, CT, false>;
+  const bool nkb7 = (p.N + 31) / 32 == 7;
+  auto kern = vec ? (nkb7 ? bwd_plane_kernel<IO, CT, true, 7> : bwd_plane_kernel<IO, CT, true, 8>)
+                  : bwd_plane_kernel<IO, CT, false, 8>;
   const size_t tab_bytes = (size_t)p.N * 64 * sizeof(float);   // LDS copy of the RoPE rows
   const int grid = persistent_grid(reinterpret_cast<const void*>(kern), kPlaneNW * 64, p.B * p.H,
                                    tab_bytes);

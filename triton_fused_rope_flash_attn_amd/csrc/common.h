@@ -432,6 +432,17 @@ __device__ __forceinline__ int xcd_remap(int L, int T) {
 
 __device__ __forceinline__ int round_up32(int x) { return (x + 31) & ~31; }
 
+// Sum over each aligned group of 8 consecutive lanes, result in every lane of
+// the group.  DPP moves inside a row (no LDS traffic): swap neighbours, swap
+// pairs (both quad permutations), then add the mirror image within the
+// 8-lane half row, which pairs each lane with one of the other quad.
+__device__ __forceinline__ float dpp_sum8(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false));  // row_half_mirror
+  return x;
+}
+
 // A copy of x the compiler cannot see through.  Index math derived from it is
 // recomputed where it is used instead of being hoisted out of the enclosing
 // loops, which keeps per-lane addresses of rarely run phases (per-plane
