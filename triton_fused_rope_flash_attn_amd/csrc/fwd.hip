@@ -317,6 +317,139 @@ fwd_kernel(const FwdParams p) {
   float m_run[QT], l_run[QT], m_thr[QT];
   f32x4 oacc[QT][DT];
 
+  // The 32-key blocks of a KV chunk run as a software pipeline over all QT
+  // subtiles of the wave.  Step j issues the LDS reads of block j+1's K-hat
+  // fragments and block j's V^T fragments, runs the softmax of block j on the
+  // VALU while the MFMA pipe still computes block j's logits, then issues the
+  // logits of block j+1 and O^T += V^T P^T of block j.  Subtiles past the last
+  // query row hold zero rows and are computed anyway: every wave of a
+  // workgroup then runs the same instruction stream with no per-subtile
+  // guards, and for the 16-row-ragged N of ViT planes the extra work lands on
+  // SIMDs that would otherwise wait at the next barrier.
+  using SAcc = f32x4[QT][2];
+  using KFr = Frag[KS][2];
+  using VFr = Frag[DT];
+  // K-hat fragments of block j: key kv = 8*(r/4) + 4*h + r%4 in A-row r of half h
+  auto load_k = [&](const S* __restrict__ cK, int j, KFr& kf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) kf[s][h] = C::lds(&cK[(32 * j + 16 * h + lr) * LDK + 32 * s + 8 * lg]);
+  };
+  // V^T fragments of block j: A = V^T rows 16d.., k-slot e <-> key 32j + 8lg + e (the P^T order)
+  auto load_v = [&](const S* __restrict__ cV, int j, VFr& vf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+      if constexpr (TRV)
+        vf[d] = C::tr(cV + tr_offset(32 * j + 8 * lg, 16 * d, LDK, lr),
+                      cV + tr_offset(32 * j + 8 * lg + 4, 16 * d, LDK, lr));
+      else
+        vf[d] = C::lds(&cV[(16 * d + lr) * LDV + vswz(16 * d + lr, 32 * j + 8 * lg)]);
+    }
+  };
+  // S^T = K-hat Q-hat^T for 32 keys (each K-hat fragment feeds QT MFMAs)
+  auto logits = [&](const KFr& kf, SAcc& sa) __attribute__((always_inline)) {
+#pragma unroll
+    for (int t = 0; t < QT; ++t) sa[t][0] = sa[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int t = 0; t < QT; ++t) sa[t][h] = C::mma(kf[s][h], qf[t][s], sa[t][h]);
+  };
+  // Online softmax of one block; the lane holds keys 8lg + (0..7) of the
+  // block for its query row.  MASKED: keys e >= lim get probability 0.
+  const float inv_c2 = 1.f / c2;
+  auto softmax = [&](auto maskc, const SAcc& sa, int lim, Frag (&pf)[QT]) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(maskc)::value;
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+      float sv[8];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[4 * h + i] = sa[t][h][i];
+      if constexpr (MASKED) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sv[e] = e < lim ? sv[e] : -INFINITY;
+      }
+      // The running max only has to bound the exponent: rescale (group max,
+      // O and row sum times 2^(m_old - m_new)) only when some lane's own max
+      // exceeds m_run + slack; m_thr = (m_run + slack) / c2 in logit units.
+      const float ml = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                             fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+      if (__any(ml > m_thr[t])) {
+        const float mx = group4_max(ml) * c2;
+        const float mnew = fmaxf(m_run[t], mx);
+        const float alpha = fast_exp2(m_run[t] - mnew);
+        l_run[t] *= alpha;
+#pragma unroll
+        for (int d = 0; d < DT; ++d) oacc[t][d] *= alpha;
+        m_run[t] = mnew;
+        m_thr[t] = (mnew + kRescaleSlack) * inv_c2;
+      }
+      float pv8[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pv8[e] = fast_exp2(__builtin_fmaf(sv[e], c2, -m_run[t]));
+        l_run[t] += pv8[e];
+      }
+      pf[t] = C::make(pv8);
+    }
+  };
+  // O^T += V^T P^T (each V^T fragment feeds QT MFMAs)
+  auto out_mma = [&](const VFr& vf, const Frag (&pf)[QT]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int t = 0; t < QT; ++t) oacc[t][d] = C::mma(vf[d], pf[t], oacc[t][d]);
+  };
+  // One KV chunk of nb blocks; the block holding key N-1 is the last one of
+  // the chunk that starts at kvb (the ragged chunk is processed first).
+  auto chunk = [&](const S* __restrict__ cK, const S* __restrict__ cV, int kvb) __attribute__((always_inline)) {
+    const int nkeys = min(KC, N - kvb);
+    const int nb = (nkeys + 31) >> 5;
+    SAcc s0, s1;
+    KFr kf;
+    VFr vf;
+    Frag pf[QT];
+    load_k(cK, 0, kf);
+    logits(kf, s0);
+    // steady state, two blocks per trip so the logits alternate between s0
+    // and s1 without register copies
+    auto step = [&](int j, const SAcc& cur, SAcc& nxt) __attribute__((always_inline)) {
+      load_k(cK, j + 1, kf);
+      load_v(cV, j, vf);
+      softmax(std::false_type{}, cur, 8, pf);
+      logits(kf, nxt);
+      out_mma(vf, pf);
+    };
+    auto last = [&](int j, const SAcc& cur) __attribute__((always_inline)) {
+      load_v(cV, j, vf);
+      if (nkeys & 31)
+        softmax(std::true_type{}, cur, N - (kvb + 32 * j + 8 * lg), pf);
+      else
+        softmax(std::false_type{}, cur, 8, pf);
+      out_mma(vf, pf);
+    };
+    int j = 0;
+    for (; j + 2 < nb; j += 2) {
+      step(j, s0, s1);
+      step(j + 1, s1, s0);
+    }
+    if (j + 1 < nb) {
+      step(j, s0, s1);
+      last(j + 1, s1);
+    } else {
+      last(j, s0);
+    }
+  };
+
+  // Without the LDS table (D = 128 or long planes), or with 32-bit I/O (twice
+  // the prefetch registers), the registers of the pipeline are not free: the
+  // same work block by block.
+  constexpr bool kPipe = kTabLds && sizeof(IO) == 2;
   // One KV chunk for all QT subtiles of the wave.  Subtiles past the last
   // query row hold zero rows and are computed anyway: every wave of a
   // workgroup then runs the same instruction stream with no per-subtile
@@ -370,7 +503,7 @@ fwd_kernel(const FwdParams p) {
 #pragma unroll
         for (int d = 0; d < DT; ++d) oacc[t][d] *= alpha;
         m_run[t] = mnew;
-        m_thr[t] = (mnew + kRescaleSlack) / c2;
+        m_thr[t] = (mnew + kRescaleSlack) * inv_c2;
       }
       float pv8[8];
 #pragma unroll
@@ -394,7 +527,7 @@ fwd_kernel(const FwdParams p) {
     }
   };
   // One KV chunk: full blocks, then the block holding key N-1 if it is ragged.
-  auto chunk = [&](const S* __restrict__ cK, const S* __restrict__ cV, int kvb) __attribute__((always_inline)) {
+  auto chunk_serial = [&](const S* __restrict__ cK, const S* __restrict__ cV, int kvb) __attribute__((always_inline)) {
     const int nkeys = min(KC, N - kvb);
     const int nfull = nkeys / 32;
     for (int j = 0; j < nfull; ++j) block(std::false_type{}, cK, cV, kvb, j);
@@ -444,7 +577,12 @@ fwd_kernel(const FwdParams p) {
       prefetch_kv(last ? (nxt >= 0 ? nxt : item) : item, last ? 0 : c + 1);
       if constexpr (FIRST) prefetch_q(nxt >= 0 ? nxt : item);
       lds_barrier();
-      if (nt > 0) chunk(sK[slot], sVt[slot], chunk_start(c));
+      if (nt > 0) {
+        if constexpr (kPipe)
+          chunk(sK[slot], sVt[slot], chunk_start(c));
+        else
+          chunk_serial(sK[slot], sVt[slot], chunk_start(c));
+      }
       ++g;
     };
     chunk_step(std::true_type{}, 0);
