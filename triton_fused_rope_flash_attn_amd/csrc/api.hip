@@ -83,6 +83,13 @@ int vec_ok(const void* p, const int64_t s[4], int es, int n_rows, int head_dim) 
   return 1;
 }
 
+// Written tensors additionally need rows that do not overlap (row stride >=
+// head_dim): the kernels then store rows >= N unconditionally and rely on
+// the descriptor range to drop them.
+int vec_out_ok(const void* p, const int64_t s[4], int es, int n_rows, int head_dim) {
+  return vec_ok(p, s, es, n_rows, head_dim) && s[2] >= head_dim;
+}
+
 void copy4(int64_t dst[4], const int64_t src[4]) {
   for (int i = 0; i < 4; ++i) dst[i] = src[i];
 }
@@ -195,7 +202,7 @@ int farope_attn_fwd(const farope_attn_desc* desc, const void* q, const int64_t q
   p.vec_q = vec_ok(q, q_stride, es, desc->seq_len, desc->head_dim);
   p.vec_k = vec_ok(k, k_stride, es, desc->seq_len, desc->head_dim);
   p.vec_v = vec_ok(v, v_stride, es, desc->seq_len, desc->head_dim);
-  p.vec_o = vec_ok(o, o_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_o = vec_out_ok(o, o_stride, es, desc->seq_len, desc->head_dim);
   p.n_blk = cdiv(p.N, fwd_block_rows(desc->head_dim));
   p.n_items = p.B * p.H * p.n_blk;
   return launch_rc(launch_fwd(p, desc->io_dtype, desc->compute_dtype, desc->head_dim,
@@ -250,8 +257,8 @@ int farope_attn_bwd_dk_dv(const farope_attn_desc* desc, const void* q, const int
   p.vec_k = vec_ok(k, k_stride, es, desc->seq_len, desc->head_dim);
   p.vec_v = vec_ok(v, v_stride, es, desc->seq_len, desc->head_dim);
   p.vec_do = vec_ok(dout, dout_stride, es, desc->seq_len, desc->head_dim);
-  p.vec_dk = vec_ok(dk, dk_stride, es, desc->seq_len, desc->head_dim);
-  p.vec_dv = vec_ok(dv, dv_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_dk = vec_out_ok(dk, dk_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_dv = vec_out_ok(dv, dv_stride, es, desc->seq_len, desc->head_dim);
   p.n_blk = cdiv(p.N, bwd_dkdv_block_rows(desc->head_dim));
   return launch_rc(launch_bwd_dkdv(p, desc->io_dtype, desc->compute_dtype, desc->head_dim,
                                    static_cast<hipStream_t>(stream)));
@@ -283,7 +290,7 @@ int farope_attn_bwd_dq(const farope_attn_desc* desc, const void* q, const int64_
   p.vec_k = vec_ok(k, k_stride, es, desc->seq_len, desc->head_dim);
   p.vec_v = vec_ok(v, v_stride, es, desc->seq_len, desc->head_dim);
   p.vec_do = vec_ok(dout, dout_stride, es, desc->seq_len, desc->head_dim);
-  p.vec_dq = vec_ok(dq, dq_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_dq = vec_out_ok(dq, dq_stride, es, desc->seq_len, desc->head_dim);
   p.n_blk = cdiv(p.N, bwd_dq_block_rows(desc->head_dim));
   return launch_rc(launch_bwd_dq(p, desc->io_dtype, desc->compute_dtype, desc->head_dim, false,
                                  static_cast<hipStream_t>(stream)));
@@ -326,9 +333,9 @@ int farope_attn_bwd(const farope_attn_desc* desc, const void* q, const int64_t q
   p.vec_v = vec_ok(v, v_stride, es, desc->seq_len, desc->head_dim);
   p.vec_o = vec_ok(o, o_stride, es, desc->seq_len, desc->head_dim);
   p.vec_do = vec_ok(dout, dout_stride, es, desc->seq_len, desc->head_dim);
-  p.vec_dq = vec_ok(dq, dq_stride, es, desc->seq_len, desc->head_dim);
-  p.vec_dk = vec_ok(dk, dk_stride, es, desc->seq_len, desc->head_dim);
-  p.vec_dv = vec_ok(dv, dv_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_dq = vec_out_ok(dq, dq_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_dk = vec_out_ok(dk, dk_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_dv = vec_out_ok(dv, dv_stride, es, desc->seq_len, desc->head_dim);
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const int D = desc->head_dim;
   if (fused) {

@@ -549,6 +549,53 @@ fwd_kernel(const FwdParams p) {
     lds_barrier();
   }
   int g = 0;   // chunks consumed so far: LDS slot g & 1
+
+  // VEC, 16-bit I/O: an item's O rows and LSE are stored during the next
+  // item, right after that item's first KV chunk has arrived.  Stores and
+  // loads share one in-order wait counter, so O stores issued at the end of
+  // an item would make the next item's waits for its prefetched Q and KV rows
+  // also wait for the stores to complete.  Deferred, the stores are older
+  // than every load waited on later and have a whole chunk of compute to
+  // drain.  The stores are unconditional: rows >= N fall outside the
+  // descriptor range and are dropped, LSE lanes lg != 0 write past their
+  // range, and before the first item the ranges are empty.
+  constexpr bool kDefer = VEC && sizeof(IO) == 2;
+  u32x2 ost[kDefer ? QT : 1][DT];
+  float olse[QT];
+  int orow[QT];
+  int oplane = -1;
+  auto flush_o = [&]() __attribute__((always_inline)) {
+    if constexpr (kDefer) {
+      const bool have = oplane >= 0;
+      const int pl = have ? oplane : 0;
+      const auto rO = make_rsrc(plane_base(p.o, p.so, pl),
+                                have ? (unsigned)(((int64_t)(N - 1) * p.so[2] + D) * ES) : 0u);
+      const auto rL = make_rsrc(p.lse + (int64_t)pl * N, have ? (unsigned)N * 4u : 0u);
+      // Lane groups lg and lg^1 trade halves so that each lane writes 8
+      // consecutive channels (16 bytes) per pair of 16-channel slices
+      // (d0, d1): v_permlane16_swap(a, b) gives even lane groups {a, a of
+      // lg+1} and odd ones {b of lg-1, b}.  Even lg then holds channels
+      // 16d0 + 4lg .. +7, odd lg channels 16d1 + 4(lg-1) .. +7.
+      const int cbase = 4 * (lg & 2);
+#pragma unroll
+      for (int t = 0; t < QT; ++t) {
+#pragma unroll
+        for (int d0 = 0; d0 < DT; d0 += 2) {
+          u32x4 w;
+#pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            const auto r = __builtin_amdgcn_permlane16_swap(ost[t][d0][k], ost[t][d0 + 1][k], false, false);
+            w[k] = r[0];
+            w[2 + k] = r[1];
+          }
+          const int ch = 16 * (d0 + (lg & 1)) + cbase;
+          __builtin_amdgcn_raw_buffer_store_b128(w, rO, (unsigned)((orow[t] * (int)p.so[2] + ch) * (int)ES), 0u, 0);
+        }
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(olse[t]), rL,
+                                              (unsigned)(lg == 0 ? orow[t] : N) * 4u, 0u, 0);
+      }
+    }
+  };
   while (item >= 0) {
     const int plane = item / p.n_blk, qb = item - plane * p.n_blk;
     const int nxt = item_of(it + 1);
@@ -573,9 +620,15 @@ fwd_kernel(const FwdParams p) {
       constexpr bool FIRST = decltype(firstc)::value;
       const int slot = g & 1;
       commit_kv(slot, chunk_start(c));
+      if constexpr (FIRST) {
+        flush_o();
+        // the next item's Q rows before the next KV chunk: Q is waited for
+        // first, at the next item's start, so at least one KV load is younger
+        // and stays in flight across that wait (also when nch == 1)
+        prefetch_q(nxt >= 0 ? nxt : item);
+      }
       const bool last = c + 1 == nch;
       prefetch_kv(last ? (nxt >= 0 ? nxt : item) : item, last ? 0 : c + 1);
-      if constexpr (FIRST) prefetch_q(nxt >= 0 ? nxt : item);
       lds_barrier();
       if (nt > 0) {
         if constexpr (kPipe)
@@ -589,26 +642,70 @@ fwd_kernel(const FwdParams p) {
     for (int c = 1; c < nch; ++c) chunk_step(std::false_type{}, c);
 
     // ---- epilogue: lane holds O[row][16d + 4lg + (0..3)] ----
-    IO* __restrict__ O = const_cast<IO*>(plane_base(p.o, p.so, plane));
+    if constexpr (kDefer) {
 #pragma unroll
-    for (int t = 0; t < QT; ++t) {
-      const float l = group4_sum(l_run[t]);
-      const int row = (qb * NW * QT + t * NW + wave) * 16 + lr;
-      if (t < nt && row < N) {
-        const float inv = 1.f / l;
+      for (int t = 0; t < QT; ++t) {
+        const float l = group4_sum(l_run[t]);
+        const float inv = __builtin_amdgcn_rcpf(l);
+#pragma unroll
+        for (int d = 0; d < DT; ++d) {
+          typedef IO io4 __attribute__((ext_vector_type(4)));
+          io4 a;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) a[r] = (IO)(oacc[t][d][r] * inv);
+          __builtin_memcpy(&ost[t][d], &a, 8);
+        }
+        olse[t] = (m_run[t] + fast_log2(l)) * kLn2;
+        orow[t] = (qb * NW * QT + t * NW + wave) * 16 + lr;
+      }
+      oplane = plane;
+    } else if constexpr (VEC) {
+      // Unconditional descriptor stores: rows >= N (every row of an inactive
+      // subtile included) fall outside the plane's range and are dropped, and
+      // the LSE of lanes lg != 0 goes to an offset past its range.  With no
+      // branch around them the wait counter keeps counting these stores
+      // exactly, so the next item's waits for its prefetched rows do not also
+      // wait for the stores to complete.
+      const auto rO = rsrc(p.o, p.so, plane);
+      const auto rL = make_rsrc(p.lse + (int64_t)plane * N, (unsigned)N * 4u);
+#pragma unroll
+      for (int t = 0; t < QT; ++t) {
+        const float l = group4_sum(l_run[t]);
+        const int row = (qb * NW * QT + t * NW + wave) * 16 + lr;
+        const float inv = __builtin_amdgcn_rcpf(l);
 #pragma unroll
         for (int d = 0; d < DT; ++d) {
           float o4[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) o4[r] = oacc[t][d][r] * inv;
-          store4(O + row * p.so[2] + (16 * d + 4 * lg) * p.so[3], p.so[3], vec_o, o4);
+          buf_store4<IO>(rO, (unsigned)((row * (int)p.so[2] + 16 * d + 4 * lg) * (int)ES), 0u, o4);
         }
-        if (lg == 0) p.lse[(int64_t)plane * N + row] = (m_run[t] + fast_log2(l)) * kLn2;
+        const float lse = (m_run[t] + fast_log2(l)) * kLn2;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(lse), rL, (unsigned)(lg == 0 ? row : N) * 4u, 0u, 0);
+      }
+    } else {
+      IO* __restrict__ O = const_cast<IO*>(plane_base(p.o, p.so, plane));
+#pragma unroll
+      for (int t = 0; t < QT; ++t) {
+        const float l = group4_sum(l_run[t]);
+        const int row = (qb * NW * QT + t * NW + wave) * 16 + lr;
+        if (t < nt && row < N) {
+          const float inv = __builtin_amdgcn_rcpf(l);
+#pragma unroll
+          for (int d = 0; d < DT; ++d) {
+            float o4[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o4[r] = oacc[t][d][r] * inv;
+            store4(O + row * p.so[2] + (16 * d + 4 * lg) * p.so[3], p.so[3], vec_o, o4);
+          }
+          if (lg == 0) p.lse[(int64_t)plane * N + row] = (m_run[t] + fast_log2(l)) * kLn2;
+        }
       }
     }
     item = nxt;
     ++it;
   }
+  flush_o();
 }
 
 // ---------------------------------------------------------------------------
