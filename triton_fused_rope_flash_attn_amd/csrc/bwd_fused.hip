@@ -404,16 +404,6 @@ bwd_plane_kernel(const BwdParams p) {
         }
       }
     }
-    // subtiles without keys < N still cover columns < nkv32 of dS^T: zero them
-#pragma unroll
-    for (int u = NUA; u < 2; ++u) {
-      const int kv0 = kw + 16 * u;
-      if (kv0 < nkv32) {
-        const Frag z = C::zero();
-        C::put4(ds + sw32(kv0 + lr, 4 * lg), z, 0);
-        C::put4(ds + sw32(kv0 + lr, 16 + 4 * lg), z, 0);
-      }
-    }
   };
 
   int it = 0;
@@ -429,11 +419,14 @@ bwd_plane_kernel(const BwdParams p) {
       const int r = i >> 4, c = i & 15;
       *reinterpret_cast<f32x4*>(&sTab[((r << 4) + (c ^ (r & 15))) * 4]) = src[i];
     }
-    // dS^T rows of keys >= round_up32(N) enter the dQ products but are never
-    // written by a sweep: zero them once, in both buffers
+    // dS^T rows of subtiles with no key < N (keys >= round_up16(N)) enter the
+    // dQ products but are never written by a sweep: zero them once, in both
+    // buffers.  (Keys >= N inside the last active subtile are written with
+    // dS = 0 by its sweep.)
+    const int nkv16 = (N + 15) & ~15;
 #pragma unroll
     for (int b = 0; b < 2; ++b)
-      for (int i = nkv32 * LDD + tid; i < kPlaneMaxN * LDD; i += kPlaneNW * 64) sdS[b][i] = S(0.f);
+      for (int i = nkv16 * LDD + tid; i < kPlaneMaxN * LDD; i += kPlaneNW * 64) sdS[b][i] = S(0.f);
   }
   while (plane >= 0) {
     const int nxt = item_of(it + 1);
@@ -480,7 +473,55 @@ bwd_plane_kernel(const BwdParams p) {
     dq(plane, nstages - 1);
     // ---- dK / dV epilogue: lane holds dV /
     //      dK-hat of key kw + 16u + lr, channels 16d + 4lg + (0..3) ----
-    {
+    if constexpr (VEC && sizeof(IO) == 2) {
+      // Unconditional 16-byte descriptor stores: keys >= N (all of an
+      // inactive subtile) fall outside the range and are dropped.  Lane
+      // groups lg and lg^1 trade halves (v_permlane16_swap) so that each lane
+      // writes 8 consecutive channels: even lg channels 16d0 + 4lg .. +7, odd
+      // lg channels 16(d0+1) + 4(lg-1) .. +7, for d0 = 0, 2.
+      const int lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+      const auto rdK = rsrc(p.dk, p.sdk, plane), rdV = rsrc(p.dv, p.sdv, plane);
+      typedef IO io4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int row = kw + 16 * u + lr;
+        const int trow = min(row, N - 1);
+#pragma unroll
+        for (int d0 = 0; d0 < 4; d0 += 2) {
+          u32x2 wv[2], wk[2];
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int d = d0 + j;
+            io4 a, g;
+            const f32x4 t = tab_chunk(sTab, trow, 4 * d + lg);   // pairs 8d + 2lg + (0, 1)
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {   // g = R^T g-hat
+              const float e = dkacc[u][d][2 * r] * p.scale, o = dkacc[u][d][2 * r + 1] * p.scale;
+              const float c = t[2 * r], sn = t[2 * r + 1];
+              g[2 * r] = (IO)(e * c + o * sn);
+              g[2 * r + 1] = (IO)(o * c - e * sn);
+              a[2 * r] = (IO)dvacc[u][d][2 * r];
+              a[2 * r + 1] = (IO)dvacc[u][d][2 * r + 1];
+            }
+            __builtin_memcpy(&wv[j], &a, 8);
+            __builtin_memcpy(&wk[j], &g, 8);
+          }
+          u32x4 xv, xk;
+#pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            const auto rv = __builtin_amdgcn_permlane16_swap(wv[0][k], wv[1][k], false, false);
+            const auto rk = __builtin_amdgcn_permlane16_swap(wk[0][k], wk[1][k], false, false);
+            xv[k] = rv[0];
+            xv[2 + k] = rv[1];
+            xk[k] = rk[0];
+            xk[2 + k] = rk[1];
+          }
+          const int ch = 16 * (d0 + (lg & 1)) + 4 * (lg & 2);
+          __builtin_amdgcn_raw_buffer_store_b128(xv, rdV, boff(p.sdv, row, ch), 0u, 0);
+          __builtin_amdgcn_raw_buffer_store_b128(xk, rdK, boff(p.sdk, row, ch), 0u, 0);
+        }
+      }
+    } else {
       const int lane = VEC ? tid & 63 : opaque(tid & 63), lr = lane & 15, lg = lane >> 4;
       IO* __restrict__ dK = const_cast<IO*>(base(p.dk, p.sdk, plane));
       IO* __restrict__ dV = const_cast<IO*>(base(p.dv, p.sdv, plane));
