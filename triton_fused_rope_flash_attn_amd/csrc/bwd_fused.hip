@@ -117,7 +117,11 @@ bwd_plane_kernel(const BwdParams p) {
     const int item = it * p.n_wg + pos;
     return item < planes ? item : -1;
   };
-  auto base = [&](const void* b, const int64_t* st, int plane) {
+  // (plane is wave-uniform; readfirstlane keeps the address arithmetic and
+  // the descriptors built from it in SGPRs even where the compiler would
+  // otherwise carry the value through a divergent branch in VGPRs)
+  auto base = [&](const void* b, const int64_t* st, int plane_) {
+    const int plane = __builtin_amdgcn_readfirstlane(plane_);
     const int bb = plane / p.H, hh = plane - bb * p.H;
     return static_cast<const IO*>(b) + bb * st[0] + hh * st[1];
   };
@@ -325,9 +329,8 @@ bwd_plane_kernel(const BwdParams p) {
         acc = C::mma(ka_tr(kb), b, acc);
     }
     const int row = qb + 16 * qt + lr;
-    if (row < N) {
-      const f32x4 t = tab_chunk(sTab, row, 4 * dd + lg);   // pairs 8dd + 2lg + (0, 1)
-      float g4[4];
+    auto unrotate = [&](int trow, float (&g4)[4]) __attribute__((always_inline)) {
+      const f32x4 t = tab_chunk(sTab, trow, 4 * dd + lg);   // pairs 8dd + 2lg + (0, 1)
 #pragma unroll
       for (int r = 0; r < 2; ++r) {   // g = R^T g-hat
         const float e = acc[2 * r] * p.scale, o = acc[2 * r + 1] * p.scale;
@@ -335,9 +338,16 @@ bwd_plane_kernel(const BwdParams p) {
         g4[2 * r] = e * c + o * sn;
         g4[2 * r + 1] = o * c - e * sn;
       }
-      if constexpr (VEC) {
-        buf_store4<IO>(rsrc(p.dq, p.sdq, plane), bdq, (unsigned)(qb * (int)p.sdq[2] * (int)ES), g4);
-      } else {
+    };
+    if constexpr (VEC) {
+      // unconditional: rows >= N fall outside the descriptor range and are dropped
+      float g4[4];
+      unrotate(min(row, N - 1), g4);
+      buf_store4<IO>(rsrc(p.dq, p.sdq, plane), bdq, (unsigned)(qb * (int)p.sdq[2] * (int)ES), g4);
+    } else if (row < N) {
+      float g4[4];
+      unrotate(row, g4);
+      {
         IO* __restrict__ dQ = const_cast<IO*>(base(p.dq, p.sdq, plane));
         store4(dQ + row * p.sdq[2] + (16 * dd + 4 * lg) * p.sdq[3], p.sdq[3], vec_dq, g4);
       }
