@@ -438,14 +438,18 @@ bwd_plane_kernel(const BwdParams p) {
     for (int b = 0; b < 2; ++b)
       for (int i = nkv16 * LDD + tid; i < kPlaneMaxN * LDD; i += kPlaneNW * 64) sdS[b][i] = S(0.f);
   }
+  // the table copy and the zeroed rows are visible
+  lds_barrier();
   while (plane >= 0) {
     const int nxt = item_of(it + 1);
-    // the previous plane's dQ tail has finished reading sK / sdS (and, on the
-    // first plane, the table copy is visible)
-    lds_barrier();
+    // No barrier is needed before these writes: the previous plane's last
+    // reads of sQ / sG / sL2 / sDl (its last sweep) precede its tail barrier,
+    // and sK is only read right after the barrier below.
     commit_kv();
     commit(0, 0);
-    // sK is complete: this wave's dQ operands
+    // sK and the first stage are complete, and every wave has finished the
+    // previous plane's dQ tail (which reads sdS) before the first sweep of
+    // this plane writes it
     lds_barrier();
     load_kq();
 #pragma unroll
@@ -456,8 +460,10 @@ bwd_plane_kernel(const BwdParams p) {
     for (int st = 0; st < nstages; ++st) {
       const int buf = st & 1;
       const int qb = st * QS;
-      if (st > 0) commit(buf, qb);
-      lds_barrier();
+      if (st > 0) {
+        commit(buf, qb);
+        lds_barrier();
+      }
       // next stage, or the next plane's first stage (the last plane re-reads its
       // own first stage).  One unconditional call with a uniformly selected
       // target: the loads land directly in the staging registers, with no

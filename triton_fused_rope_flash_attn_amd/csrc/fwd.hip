@@ -173,12 +173,18 @@ fwd_kernel(const FwdParams p) {
   float pcs[ITER][2][kTabLds ? 1 : 8];
   auto prefetch_kv = [&](int item, int c) __attribute__((always_inline)) {
     const int plane = item / p.n_blk;
-    if constexpr (VEC && kTabLds && UNITS % NT == 0) {
+    if constexpr (VEC && kTabLds && UNITS % 64 == 0) {
+      // every wave loads whole units or none (UNITS is a multiple of the wave
+      // size): a wave without a unit gets empty-range descriptors, so its
+      // loads stay unconditional and return zeros without memory traffic
       const int kvb = chunk_start(c);
-      const auto rK = rsrc(p.k, p.sk, plane), rV = rsrc(p.v, p.sv, plane);
 #pragma unroll
       for (int it = 0; it < ITER; ++it) {
-        const int u = tid + it * NT;
+        const int u0 = tid + it * NT;
+        const bool act = UNITS % NT == 0 || u0 < UNITS;   // wave-uniform
+        const int u = act ? u0 : 0;
+        const auto rK = make_rsrc(plane_base(p.k, p.sk, plane), act ? (unsigned)(((int64_t)(N - 1) * p.sk[2] + D) * ES) : 0u);
+        const auto rV = make_rsrc(plane_base(p.v, p.sv, plane), act ? (unsigned)(((int64_t)(N - 1) * p.sv[2] + D) * ES) : 0u);
         const int rp = u / CPR, cc = u - rp * CPR;
 #pragma unroll
         for (int x = 0; x < 2; ++x) {
