@@ -13,9 +13,9 @@
 // their dK-hat / dV accumulators in registers.  The rotated K-hat rows of the
 // whole plane also stay in LDS (row-major), from which the K-hat^T operand of
 // dQ-hat^T = K-hat^T dS^T is read transposed.  The plane's queries are swept in
-// stages of 64 rows, double-buffered in LDS, one barrier per stage:
+// stages of 32 rows, double-buffered in LDS, one barrier per stage:
 //   commit   staged registers -> LDS: Q-hat and dO rows (row-major),
-//            LSE*log2(e), delta = rowsum(dO*O)
+//            LSE*log2(e), -delta = -rowsum(dO*O)
 //   barrier
 //   prefetch next stage's Q, dO, O rows (+ RoPE table rows, LSE)
 //   dQ of the previous stage: dQ-hat^T = K-hat^T dS^T from the resident
@@ -195,7 +195,7 @@ bwd_plane_kernel(const BwdParams p) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) d += g[e] * o[e];
       d = dpp_sum8(d);
-      if (sc == 0) sDl[buf][sr] = d;
+      if (sc == 0) sDl[buf][sr] = -d;   // stored negated: it seeds the dP accumulators
     } else if (t - 256 < QS) {
       sL2[buf][t - 256] = qb + (t - 256) < N ? plse * kLog2e : INFINITY;
     }
@@ -310,15 +310,16 @@ bwd_plane_kernel(const BwdParams p) {
   //      NKB = number of 32-key blocks (straight-line code, no per-block branch) ----
   // VEC lane byte offset of this lane's dQ element (row 16qt + lr of a stage, channel 16dd + 4lg)
   const unsigned bdq = VEC ? boff(p.sdq, 16 * qt + lr, 16 * dd + 4 * lg) : 0u;
+  // lane parts of the transposed dS^T read offsets (as for kq), kept for the
+  // whole kernel: per stage only the buffer base changes
+  const int dqr0 = 8 * lg + (lr >> 2);
+  const int dqo0 = sw32(dqr0, 16 * qt + 4 * (lr & 3)), dqo1 = sw32(dqr0 + 4, 16 * qt + 4 * (lr & 3));
   auto dq = [&](int plane, int sp) __attribute__((always_inline)) {
-    const int lane = opaque(tid & 63), lr = lane & 15, lg = lane >> 4;
     const int buf = sp & 1;
     const int qb = sp * QS;
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    // lane parts of the transposed-read offsets as for kq
-    const int r0 = 8 * lg + (lr >> 2);
-    const S* db0 = &sdS[buf][sw32(r0, 16 * qt + 4 * (lr & 3))];
-    const S* db1 = &sdS[buf][sw32(r0 + 4, 16 * qt + 4 * (lr & 3))];
+    const S* db0 = &sdS[buf][dqo0];
+    const S* db1 = &sdS[buf][dqo1];
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
       // A = K-hat^T rows 16dd.., B = dS^T columns 16qt..; k = keys 32kb + 8lg + (0..7)
@@ -366,14 +367,14 @@ bwd_plane_kernel(const BwdParams p) {
       for (int h = 0; h < 2; ++h) {
         const int q0 = 16 * h + 4 * lg;   // queries q0 .. q0+3 in this lane
         const f32x4 l2 = *reinterpret_cast<const f32x4*>(&sL2[buf][q0]);
-        const f32x4 dl = *reinterpret_cast<const f32x4*>(&sDl[buf][q0]);
+        const f32x4 ndl = *reinterpret_cast<const f32x4*>(&sDl[buf][q0]);   // -delta
         // accumulators start at the key mask (S) and at -delta (dP), so that
         // P = exp2(S*c2 - l2) is 0 for keys >= N and dP - delta needs no extra op
         f32x4 sacc[NUA], pacc[NUA];
 #pragma unroll
         for (int u = 0; u < NUA; ++u) {
           sacc[u] = kmask[u];
-          pacc[u] = -dl;
+          pacc[u] = ndl;
         }
         const int qr = 16 * h + lr;
 #pragma unroll
