@@ -179,22 +179,22 @@ bwd_plane_kernel(const BwdParams p) {
   auto commit = [&](int buf, int qb) __attribute__((always_inline)) {
     const int t = tid, sr = ssr, sc = ssc;
     if (t < 256) {
-      float x[8], g[8], o[8];
+      float x[8], g[8];
       unpack8(pq, x);
-      unpack8(pg, g);
-      unpack8(po, o);
       // Q-hat = R q (rows >= N are zero either way)
       const int row = min(qb + sr, N - 1);
       const f32x4 c0 = tab_chunk(sTab, row, 2 * sc), c1 = tab_chunk(sTab, row, 2 * sc + 1);
       const float cs[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
       rope_rotate8(x, cs);
       C::put8(&sQ[buf][sw64(sr, 8 * sc)], x);
-      C::put8(&sG[buf][sw64(sr, 8 * sc)], g);
+      if constexpr (std::is_same<IO, S>::value) {
+        *reinterpret_cast<typename Raw8<IO>::vec*>(&sG[buf][sw64(sr, 8 * sc)]) = pg.v;   // raw dO row segment
+      } else {
+        unpack8(pg, g);
+        C::put8(&sG[buf][sw64(sr, 8 * sc)], g);
+      }
       // delta = rowsum(dO * O); the 8 chunks of a row are 8 consecutive lanes
-      float d = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) d += g[e] * o[e];
-      d = dpp_sum8(d);
+      const float d = dpp_sum8(dot8(pg, po, 0.f));
       if (sc == 0) sDl[buf][sr] = -d;   // stored negated: it seeds the dP accumulators
     } else if (t - 256 < QS) {
       sL2[buf][t - 256] = qb + (t - 256) < N ? plse * kLog2e : INFINITY;

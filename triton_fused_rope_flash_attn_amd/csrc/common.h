@@ -17,6 +17,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <stdint.h>
 
 namespace farope {
@@ -431,6 +432,29 @@ __device__ __forceinline__ int xcd_remap(int L, int T) {
 }
 
 __device__ __forceinline__ int round_up32(int x) { return (x + 31) & ~31; }
+
+// sum_e a[e] * b[e] over an 8-element row segment, plus c, in fp32.  16-bit
+// types use the packed dot instructions (v_dot2c_f32_{bf16,f16}) on the raw
+// registers; the products of 16-bit values are exact in fp32 either way.
+template <typename IO>
+__device__ __forceinline__ float dot8(const Raw8<IO>& a, const Raw8<IO>& b, float c) {
+  if constexpr (sizeof(IO) == 2) {
+    typedef IO io2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const io2 x = {a.v[2 * e], a.v[2 * e + 1]}, y = {b.v[2 * e], b.v[2 * e + 1]};
+      if constexpr (std::is_same<IO, bf16>::value)
+        c = __builtin_amdgcn_fdot2_f32_bf16(x, y, c, false);
+      else
+        c = __builtin_amdgcn_fdot2(x, y, c, false);
+    }
+    return c;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) c = __builtin_fmaf((float)a.v[e], (float)b.v[e], c);
+    return c;
+  }
+}
 
 // Sum over each aligned group of 8 consecutive lanes, result in every lane of
 // the group.  DPP moves inside a row (no LDS traffic): swap neighbours, swap
