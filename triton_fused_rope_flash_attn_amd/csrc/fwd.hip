@@ -417,18 +417,23 @@ fwd_kernel(const FwdParams p) {
     const int nkeys = min(KC, N - kvb);
     const int nb = (nkeys + 31) >> 5;
     SAcc s0, s1;
-    KFr kf;
+    KFr ka, kb;
     VFr vf;
     Frag pf[QT];
-    load_k(cK, 0, kf);
-    logits(kf, s0);
-    // steady state, two blocks per trip so the logits alternate between s0
-    // and s1 without register copies
-    auto step = [&](int j, const SAcc& cur, SAcc& nxt) __attribute__((always_inline)) {
-      load_k(cK, j + 1, kf);
+    load_k(cK, 0, ka);
+    logits(ka, s0);
+    load_k(cK, min(1, nb - 1), kb);
+    // Step j: the logits of block j+1 (its K-hat is already in registers) go
+    // to the MFMA pipe first and run under block j's softmax; block j+2's
+    // K-hat (into the registers block j's K-hat has left) and block j's V^T
+    // load meanwhile.  Two blocks per trip, so the logits and K-hat registers
+    // alternate without copies; past the last block the K-hat load re-reads
+    // the last block.
+    auto step = [&](int j, const SAcc& cur, SAcc& nxt, const KFr& kn, KFr& kfree) __attribute__((always_inline)) {
+      logits(kn, nxt);
+      load_k(cK, min(j + 2, nb - 1), kfree);
       load_v(cV, j, vf);
       softmax(std::false_type{}, cur, 8, pf);
-      logits(kf, nxt);
       out_mma(vf, pf);
     };
     auto last = [&](int j, const SAcc& cur) __attribute__((always_inline)) {
@@ -441,11 +446,14 @@ fwd_kernel(const FwdParams p) {
     };
     int j = 0;
     for (; j + 2 < nb; j += 2) {
-      step(j, s0, s1);
-      step(j + 1, s1, s0);
+      step(j, s0, s1, kb, ka);
+      step(j + 1, s1, s0, ka, kb);
     }
     if (j + 1 < nb) {
-      step(j, s0, s1);
+      logits(kb, s1);
+      load_v(cV, j, vf);
+      softmax(std::false_type{}, s0, 8, pf);
+      out_mma(vf, pf);
       last(j + 1, s1);
     } else {
       last(j, s0);
