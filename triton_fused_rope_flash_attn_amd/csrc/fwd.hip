@@ -366,43 +366,69 @@ fwd_kernel(const FwdParams p) {
   };
   // Online softmax of one block; the lane holds keys 8lg + (0..7) of the
   // block for its query row.  MASKED: keys e >= lim get probability 0.
+  // The running max only has to bound the exponent: O and the row sum are
+  // rescaled (group max, times 2^(m_old - m_new)) only when some lane's own
+  // max exceeds m_run + slack; m_thr = (m_run + slack) / c2 in logit units.
+  //
+  // The common case has no branch: soft() computes P with the current
+  // running max and reports whether any row crossed its threshold; only then
+  // does fixup() rescale and recompute the block (rare after an item's first
+  // block).  Straight-line code lets the scheduler interleave these VALU
+  // instructions with the MFMAs of the neighbouring blocks.
   const float inv_c2 = 1.f / c2;
-  auto softmax = [&](auto maskc, const SAcc& sa, int lim, Frag (&pf)[QT]) __attribute__((always_inline)) {
-    constexpr bool MASKED = decltype(maskc)::value;
+  auto block_vals = [&](auto maskc, const SAcc& sa, int t, int lim, float (&sv)[8]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sv[4 * h + i] = sa[t][h][i];
+    if constexpr (decltype(maskc)::value) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sv[e] = e < lim ? sv[e] : -INFINITY;
+    }
+  };
+  auto max8 = [](const float (&sv)[8]) __attribute__((always_inline)) {
+    return fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+  };
+  auto probs = [&](const float (&sv)[8], int t, Frag& pft) __attribute__((always_inline)) {
+    float pv8[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      pv8[e] = fast_exp2(__builtin_fmaf(sv[e], c2, -m_run[t]));
+      l_run[t] += pv8[e];
+    }
+    pft = C::make(pv8);
+  };
+  auto soft = [&](auto maskc, const SAcc& sa, int lim, Frag (&pf)[QT], float (&lkeep)[QT]) __attribute__((always_inline)) {
+    bool need = false;
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
       float sv[8];
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sv[4 * h + i] = sa[t][h][i];
-      if constexpr (MASKED) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sv[e] = e < lim ? sv[e] : -INFINITY;
-      }
-      // The running max only has to bound the exponent: rescale (group max,
-      // O and row sum times 2^(m_old - m_new)) only when some lane's own max
-      // exceeds m_run + slack; m_thr = (m_run + slack) / c2 in logit units.
-      const float ml = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                             fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-      if (__any(ml > m_thr[t])) {
-        const float mx = group4_max(ml) * c2;
-        const float mnew = fmaxf(m_run[t], mx);
-        const float alpha = fast_exp2(m_run[t] - mnew);
-        l_run[t] *= alpha;
-#pragma unroll
-        for (int d = 0; d < DT; ++d) oacc[t][d] *= alpha;
-        m_run[t] = mnew;
-        m_thr[t] = (mnew + kRescaleSlack) * inv_c2;
-      }
-      float pv8[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        pv8[e] = fast_exp2(__builtin_fmaf(sv[e], c2, -m_run[t]));
-        l_run[t] += pv8[e];
-      }
-      pf[t] = C::make(pv8);
+      block_vals(maskc, sa, t, lim, sv);
+      need |= __any(max8(sv) > m_thr[t]);
+      lkeep[t] = l_run[t];
+      probs(sv, t, pf[t]);
     }
+    return need;
+  };
+  auto fixup = [&](auto maskc, const SAcc& sa, int lim, Frag (&pf)[QT], const float (&lkeep)[QT]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+      float sv[8];
+      block_vals(maskc, sa, t, lim, sv);
+      const float mx = group4_max(max8(sv)) * c2;
+      const float mnew = fmaxf(m_run[t], mx);
+      const float alpha = fast_exp2(m_run[t] - mnew);
+      l_run[t] = lkeep[t] * alpha;
+#pragma unroll
+      for (int d = 0; d < DT; ++d) oacc[t][d] *= alpha;
+      m_run[t] = mnew;
+      m_thr[t] = (mnew + kRescaleSlack) * inv_c2;
+      probs(sv, t, pf[t]);
+    }
+  };
+  auto softmax = [&](auto maskc, const SAcc& sa, int lim, Frag (&pf)[QT]) __attribute__((always_inline)) {
+    float lkeep[QT];
+    if (soft(maskc, sa, lim, pf, lkeep)) fixup(maskc, sa, lim, pf, lkeep);
   };
   // O^T += V^T P^T (each V^T fragment feeds QT MFMAs)
   auto out_mma = [&](const VFr& vf, const Frag (&pf)[QT]) __attribute__((always_inline)) {
