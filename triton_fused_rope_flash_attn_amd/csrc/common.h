@@ -129,8 +129,13 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kBufWord3 = 0x00020000;   // raw buffer, 32-bit data format (gfx9 family)
 
+// The base and size must be wave-uniform.  The size passes through
+// readfirstlane so that the descriptor is built in SGPRs even where the
+// compiler holds the uniform value in VGPRs; a descriptor in VGPRs turns every
+// access through it into a loop over the distinct lane values.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufWord3);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                           __builtin_amdgcn_readfirstlane((int)bytes), kBufWord3);
 }
 
 // 8 elements at byte offset voff + soff
