@@ -354,14 +354,21 @@ bwd_plane_kernel(const BwdParams p) {
       }
     }
   };
-  // ---- S, dP, P, dS, dV, dK for the wave's first NUA subtiles over one
-  //      32-query stage (query rows in natural order, see above) ----
-  auto sweep_keys = [&](auto nuc, int buf) __attribute__((always_inline)) {
-    constexpr int NUA = decltype(nuc)::value;
+  // ---- S, dP, P, dS, dV, dK for the wave's two subtiles over one 32-query
+  //      stage (query rows in natural order, see above).  A wave whose second
+  //      subtile has no key < N sweeps it too: its S accumulators start at
+  //      -inf and its K / V rows are zero, so P = dS = 0 there and its dK / dV
+  //      accumulators stay 0.  One code path for every active wave keeps the
+  //      dK / dV accumulators in the same registers across stages (a per-wave
+  //      choice between sweep variants makes the compiler copy all of them at
+  //      the join every stage), and a wave with one live subtile shares its
+  //      SIMD with a fully loaded one anyway. ----
+  auto sweep_keys = [&](int buf) __attribute__((always_inline)) {
+    constexpr int NUA = 2;
     const S* q = &sQ[buf][0];
     const S* g = &sG[buf][0];
     S* ds = &sdS[buf][0];
-    if constexpr (NUA > 0) {
+    {
       Frag pf[NUA], dsf[NUA];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
@@ -430,14 +437,13 @@ bwd_plane_kernel(const BwdParams p) {
       const int r = i >> 4, c = i & 15;
       *reinterpret_cast<f32x4*>(&sTab[((r << 4) + (c ^ (r & 15))) * 4]) = src[i];
     }
-    // dS^T rows of subtiles with no key < N (keys >= round_up16(N)) enter the
+    // dS^T rows of waves with no key < N (keys >= round_up32(N)) enter the
     // dQ products but are never written by a sweep: zero them once, in both
-    // buffers.  (Keys >= N inside the last active subtile are written with
-    // dS = 0 by its sweep.)
-    const int nkv16 = (N + 15) & ~15;
+    // buffers.  (Keys >= N of an active wave are written with dS = 0 by its
+    // sweep.)
 #pragma unroll
     for (int b = 0; b < 2; ++b)
-      for (int i = nkv16 * LDD + tid; i < kPlaneMaxN * LDD; i += kPlaneNW * 64) sdS[b][i] = S(0.f);
+      for (int i = nkv32 * LDD + tid; i < kPlaneMaxN * LDD; i += kPlaneNW * 64) sdS[b][i] = S(0.f);
   }
   // the table copy and the zeroed rows are visible
   lds_barrier();
@@ -474,13 +480,7 @@ bwd_plane_kernel(const BwdParams p) {
         prefetch(last ? (nxt >= 0 ? nxt : plane) : plane, last ? 0 : qb + QS);
       }
       if (st > 0) dq(plane, st - 1);
-      if (nu == 2) {
-        sweep_keys(std::integral_constant<int, 2>{}, buf);
-      } else if (nu == 1) {
-        sweep_keys(std::integral_constant<int, 1>{}, buf);
-      } else {
-        sweep_keys(std::integral_constant<int, 0>{}, buf);
-      }
+      if (nu > 0) sweep_keys(buf);
     }
 
     // kf / vf are dead: start the next plane's own K / V rows, then finish this
