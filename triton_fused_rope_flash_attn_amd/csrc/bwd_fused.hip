@@ -150,12 +150,24 @@ bwd_plane_kernel(const BwdParams p) {
     bg = boff(p.sdo, ssr, 8 * ssc);
     bo = boff(p.so, ssr, 8 * ssc);
   }
-  auto prefetch = [&](int plane, int qb) __attribute__((always_inline)) {
+  // Buffer descriptors of the staged rows of one plane (SGPRs).  They are
+  // built once per plane, in the last stage of the previous plane, whose
+  // prefetch is the first to read the plane, instead of per stage (the (b, h)
+  // split of the plane index and the 64-bit base arithmetic are most of a
+  // stage's scalar work).
+  struct StageRs {
+    __amdgpu_buffer_rsrc_t q, g, o, l;
+  };
+  auto stage_rs = [&](int plane) __attribute__((always_inline)) {
+    return StageRs{rsrc(p.q, p.sq, plane), rsrc(p.dout, p.sdo, plane), rsrc(p.o, p.so, plane),
+                   make_rsrc(p.lse + (int64_t)plane * N, (unsigned)N * 4u)};
+  };
+  auto prefetch = [&](int plane, const StageRs& rs, int qb) __attribute__((always_inline)) {
     if constexpr (VEC) {
       if (tid < 256) {   // waves 0..3 (wave-uniform)
-        pq = buf_load8<IO>(rsrc(p.q, p.sq, plane), bq, (unsigned)(qb * (int)p.sq[2] * (int)ES));
-        pg = buf_load8<IO>(rsrc(p.dout, p.sdo, plane), bg, (unsigned)(qb * (int)p.sdo[2] * (int)ES));
-        po = buf_load8<IO>(rsrc(p.o, p.so, plane), bo, (unsigned)(qb * (int)p.so[2] * (int)ES));
+        pq = buf_load8<IO>(rs.q, bq, (unsigned)(qb * (int)p.sq[2] * (int)ES));
+        pg = buf_load8<IO>(rs.g, bg, (unsigned)(qb * (int)p.sdo[2] * (int)ES));
+        po = buf_load8<IO>(rs.o, bo, (unsigned)(qb * (int)p.so[2] * (int)ES));
       }
     } else {
       const int t = opaque(tid), sr = (t >> 3) & 31, sc = t & 7, gr = qb + sr;
@@ -171,10 +183,8 @@ bwd_plane_kernel(const BwdParams p) {
     // wait on this load would also drain the Q / dO / O loads issued above);
     // the buffer range is the plane's N values, rows >= N read 0
     const int lt = tid - 256;
-    if (lt >= 0 && lt < QS) {
-      const auto rl = make_rsrc(p.lse + (int64_t)plane * N, (unsigned)N * 4u);
-      plse = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rl, (unsigned)lt * 4u, (unsigned)qb * 4u, 0));
-    }
+    if (lt >= 0 && lt < QS)
+      plse = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs.l, (unsigned)lt * 4u, (unsigned)qb * 4u, 0));
   };
   auto commit = [&](int buf, int qb) __attribute__((always_inline)) {
     const int t = tid, sr = ssr, sc = ssc;
@@ -314,7 +324,7 @@ bwd_plane_kernel(const BwdParams p) {
   // whole kernel: per stage only the buffer base changes
   const int dqr0 = 8 * lg + (lr >> 2);
   const int dqo0 = sw32(dqr0, 16 * qt + 4 * (lr & 3)), dqo1 = sw32(dqr0 + 4, 16 * qt + 4 * (lr & 3));
-  auto dq = [&](int plane, int sp) __attribute__((always_inline)) {
+  auto dq = [&](int plane, __amdgpu_buffer_rsrc_t rdq, int sp) __attribute__((always_inline)) {
     const int buf = sp & 1;
     const int qb = sp * QS;
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -344,7 +354,7 @@ bwd_plane_kernel(const BwdParams p) {
       // unconditional: rows >= N fall outside the descriptor range and are dropped
       float g4[4];
       unrotate(min(row, N - 1), g4);
-      buf_store4<IO>(rsrc(p.dq, p.sdq, plane), bdq, (unsigned)(qb * (int)p.sdq[2] * (int)ES), g4);
+      buf_store4<IO>(rdq, bdq, (unsigned)(qb * (int)p.sdq[2] * (int)ES), g4);
     } else if (row < N) {
       float g4[4];
       unrotate(row, g4);
@@ -427,7 +437,8 @@ bwd_plane_kernel(const BwdParams p) {
   int it = 0;
   int plane = item_of(0);
   if (plane < 0) return;
-  prefetch(plane, 0);
+  StageRs rs = stage_rs(plane);
+  prefetch(plane, rs, 0);
   prefetch_kv(plane);
   {
     // table rows shift .. N-1+shift of the packed table -> sTab (token order, swizzled)
@@ -449,6 +460,7 @@ bwd_plane_kernel(const BwdParams p) {
   lds_barrier();
   while (plane >= 0) {
     const int nxt = item_of(it + 1);
+    const auto rdq = rsrc(p.dq, p.sdq, plane);   // (VEC)
     // No barrier is needed before these writes: the previous plane's last
     // reads of sQ / sG / sL2 / sDl (its last sweep) precede its tail barrier,
     // and sK is only read right after the barrier below.
@@ -477,9 +489,11 @@ bwd_plane_kernel(const BwdParams p) {
       // merge copies that would force an early wait on them.
       {
         const bool last = st + 1 == nstages;
-        prefetch(last ? (nxt >= 0 ? nxt : plane) : plane, last ? 0 : qb + QS);
+        const int tp = last ? (nxt >= 0 ? nxt : plane) : plane;
+        if (last) rs = stage_rs(tp);
+        prefetch(tp, rs, last ? 0 : qb + QS);
       }
-      if (st > 0) dq(plane, st - 1);
+      if (st > 0) dq(plane, rdq, st - 1);
       if (nu > 0) sweep_keys(buf);
     }
 
@@ -487,7 +501,7 @@ bwd_plane_kernel(const BwdParams p) {
     // plane: dQ of the last stage, dK / dV
     prefetch_kv(nxt >= 0 ? nxt : plane);
     lds_barrier();
-    dq(plane, nstages - 1);
+    dq(plane, rdq, nstages - 1);
     // ---- dK / dV epilogue: lane holds dV /
     //      dK-hat of key kw + 16u + lr, channels 16d + 4lg + (0..3) ----
     if constexpr (VEC && sizeof(IO) == 2) {
