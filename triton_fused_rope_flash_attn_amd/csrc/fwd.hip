@@ -171,8 +171,37 @@ fwd_kernel(const FwdParams p) {
   //      (+ their cos/sin when the table is not in LDS) ----
   Raw8<IO> pk[ITER][2], pv[ITER][2];
   float pcs[ITER][2][kTabLds ? 1 : 8];
-  auto prefetch_kv = [&](int item, int c) __attribute__((always_inline)) {
+  // K / V buffer descriptors of one item's plane (SGPRs), built once per item
+  // -- in the previous item's last chunk, whose prefetch is the first to read
+  // the item -- instead of per chunk (the plane split and the 64-bit base
+  // arithmetic are most of a chunk's scalar work).  Used when every wave
+  // loads whole units (UNITS a multiple of the workgroup size).
+  struct KvRs {
+    __amdgpu_buffer_rsrc_t k, v;
+  };
+  auto kv_rs = [&](int item) __attribute__((always_inline)) {
     const int plane = item / p.n_blk;
+    return KvRs{rsrc(p.k, p.sk, plane), rsrc(p.v, p.sv, plane)};
+  };
+  auto prefetch_kv = [&](int item, const KvRs& kr, int c) __attribute__((always_inline)) {
+    const int plane = item / p.n_blk;
+    if constexpr (VEC && kTabLds && UNITS % NT == 0) {
+      const int kvb = chunk_start(c);
+#pragma unroll
+      for (int it = 0; it < ITER; ++it) {
+        const int u = tid + it * NT;
+        const int rp = u / CPR, cc = u - rp * CPR;
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+          const int r = 2 * rp + x;
+          pk[it][x] = buf_load8<IO>(kr.k, (unsigned)((r * (int)p.sk[2] + 8 * cc) * (int)ES),
+                                    (unsigned)(kvb * (int)p.sk[2] * (int)ES));
+          pv[it][x] = buf_load8<IO>(kr.v, (unsigned)((r * (int)p.sv[2] + 8 * cc) * (int)ES),
+                                    (unsigned)(kvb * (int)p.sv[2] * (int)ES));
+        }
+      }
+      return;
+    }
     if constexpr (VEC && kTabLds && UNITS % 64 == 0) {
       // every wave loads whole units or none (UNITS is a multiple of the wave
       // size): a wave without a unit gets empty-range descriptors, so its
@@ -577,7 +606,8 @@ fwd_kernel(const FwdParams p) {
   int it = 0;
   int item = item_of(0);
   if (item < 0) return;
-  prefetch_kv(item, 0);
+  KvRs kvr = kv_rs(item);
+  prefetch_kv(item, kvr, 0);
   prefetch_q(item);
   if constexpr (kTabLds) {
     // rows 0 .. N-1+shift of the packed table (TCH 16-byte chunks each), swizzled
@@ -668,7 +698,9 @@ fwd_kernel(const FwdParams p) {
         prefetch_q(nxt >= 0 ? nxt : item);
       }
       const bool last = c + 1 == nch;
-      prefetch_kv(last ? (nxt >= 0 ? nxt : item) : item, last ? 0 : c + 1);
+      const int tgt = last ? (nxt >= 0 ? nxt : item) : item;
+      if (last) kvr = kv_rs(tgt);
+      prefetch_kv(tgt, kvr, last ? 0 : c + 1);
       lds_barrier();
       if (nt > 0) {
         if constexpr (kPipe)
