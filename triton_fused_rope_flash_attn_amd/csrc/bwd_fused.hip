@@ -330,14 +330,19 @@ bwd_plane_kernel(const BwdParams p) {
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
     const S* db0 = &sdS[buf][dqo0];
     const S* db1 = &sdS[buf][dqo1];
+    // A = K-hat^T rows 16dd.., B = dS^T columns 16qt..; k = keys 32kb + 8lg + (0..7).
+    // The B fragment of block kb+1 is read before the product of block kb,
+    // so each product waits for a read issued one product earlier rather
+    // than for a full LDS round trip.
+    Frag b2[2];
+    b2[0] = C::tr(db0, db1);
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
-      // A = K-hat^T rows 16dd.., B = dS^T columns 16qt..; k = keys 32kb + 8lg + (0..7)
-      const Frag b = C::tr(db0 + 32 * kb * LDD, db1 + 32 * kb * LDD);
+      if (kb + 1 < NKB) b2[(kb + 1) & 1] = C::tr(db0 + 32 * (kb + 1) * LDD, db1 + 32 * (kb + 1) * LDD);
       if constexpr (KQREG)
-        acc = C::mma(kq[kb], b, acc);
+        acc = C::mma(kq[kb], b2[kb & 1], acc);
       else
-        acc = C::mma(ka_tr(kb), b, acc);
+        acc = C::mma(ka_tr(kb), b2[kb & 1], acc);
     }
     const int row = qb + 16 * qt + lr;
     auto unrotate = [&](int trow, float (&g4)[4]) __attribute__((always_inline)) {
