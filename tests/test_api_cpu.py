@@ -103,6 +103,9 @@ def test_fake_kernels_shapes_and_dtypes():
         dq, dk, dv = torch.ops.farope.attn_bwd(q, q, q, q, o, lse, rope, 196, True, 0.125, 2)
         for t in (dq, dk, dv):
             assert t.shape == q.shape and t.dtype == q.dtype
+        cosp = torch.empty(196, 32, dtype=torch.float32, device="cuda")
+        packed = torch.ops.farope.rope_pack(cosp, cosp)
+        assert packed.shape == (197 * 32 * 2,) and packed.dtype == torch.float32
 
 
 def test_custom_ops_registered_with_autograd():

@@ -271,3 +271,29 @@ def test_large_logits_finite():
         omx, omn = errors(other[i], ref[i])
         _say(f"[x4 inputs] {name}: ours max {mx:.3e} mean {mn:.3e} | torch-bf16 max {omx:.3e} mean {omn:.3e}")
         assert mn <= 1.25 * omn + 1e-4, name
+
+
+def test_torch_compile_fullgraph():
+    """The ops trace as opaque nodes: torch.compile(fullgraph=True) of the public
+    entry (RoPE table packing included) matches eager bit for bit, fwd and bwd."""
+    import torch._dynamo
+
+    cfg = dict(CONFIGS["vit_b"], B=2)
+    q, k, v, do = make_inputs(cfg, DEV)
+    table = CosSinTable(ROPE_BASE, 14, 64, device=DEV)
+
+    def f(q, k, v):
+        return sdpa_triton_fa_rope(q, k, v, table)
+
+    torch._dynamo.reset()
+    cf = torch.compile(f, fullgraph=True, backend="aot_eager")
+    outs = []
+    for fn in (f, cf):
+        qq, kk, vv = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+        o = fn(qq, kk, vv)
+        o.backward(do)
+        torch.cuda.synchronize()
+        outs.append((o.detach(), qq.grad, kk.grad, vv.grad))
+    for name, a, b in zip(("O", "dQ", "dK", "dV"), *outs):
+        _say(f"[compile] {name}: equal={torch.equal(a, b)}")
+        assert torch.equal(a, b), name

@@ -56,7 +56,6 @@ def build_axial_rope_pairs(
 
 def pack_rope_tables(cosp: torch.Tensor, sinp: torch.Tensor) -> torch.Tensor:
     """Kernel layout of (COSP, SINP): fp32 [(n_pos+1) * D/2 * 2] on their GPU."""
-    from . import _lib
 
     if cosp.dim() != 2 or sinp.shape != cosp.shape:
         raise ValueError(
@@ -69,10 +68,24 @@ def pack_rope_tables(cosp: torch.Tensor, sinp: torch.Tensor) -> torch.Tensor:
             "farope runs on ROCm GPUs only: the RoPE tables must live on the GPU "
             f"(got {cosp.device} / {sinp.device})"
         )
+    return torch.ops.farope.rope_pack(cosp, sinp)
+
+
+@torch.library.custom_op("farope::rope_pack", mutates_args=())
+def _rope_pack_op(cosp: torch.Tensor, sinp: torch.Tensor) -> torch.Tensor:
+    """``farope_rope_pack`` as an opaque op, so the packing also traces under torch.compile."""
+    from . import _lib
+
     n_pos, d2 = cosp.shape
     out = torch.empty((n_pos + 1) * d2 * 2, dtype=torch.float32, device=cosp.device)
     _lib.rope_pack(cosp, sinp, out)
     return out
+
+
+@_rope_pack_op.register_fake
+def _rope_pack_fake(cosp, sinp):
+    n_pos, d2 = cosp.shape
+    return cosp.new_empty(((n_pos + 1) * d2 * 2,))
 
 
 class CosSinTable(torch.nn.Module):
@@ -105,8 +118,15 @@ class CosSinTable(torch.nn.Module):
         return side
 
     def packed(self) -> torch.Tensor:
-        """Kernel-layout table, rebuilt when COSP/SINP change (storage, version, device)."""
+        """Kernel-layout table, rebuilt when COSP/SINP change (storage, version, device).
+
+        Under ``torch.compile`` the table is packed inside the graph on every call
+        (one small kernel): the cache key reads storage pointers, which traced
+        tensors do not have.
+        """
         c, s = self.COSP, self.SINP
+        if torch.compiler.is_compiling():
+            return pack_rope_tables(c, s)
         key = (c.data_ptr(), c._version, s.data_ptr(), s._version, c.device, tuple(c.shape))
         if self._packed is None or self._packed_key != key:
             self._packed = pack_rope_tables(c, s)
