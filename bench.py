@@ -179,6 +179,55 @@ def time_torch_rocm(wl, steps, warmup):
             "what": "Python 2D RoPE (bf16) + F.scaled_dot_product_attention (flash/efficient), fwd+bwd"}
 
 
+def time_block(wl, steps, warmup):
+    """ViT attention sub-layer (qkv Linear -> op -> proj), eager fwd+bwd, bf16:
+    ``RoPEAttention`` with the fused op vs the same layer and weights with
+    Python RoPE + torch SDPA (flash/efficient) in its place."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    from oracle import torch_ref
+    from triton_fused_rope_flash_attn_amd import RoPEAttention
+
+    def torch_attn(q, k, v, table, H_img=None, has_cls=True):
+        cosp, sinp = table.tables()
+        qh = torch_ref.apply_rope(q, cosp, sinp, has_cls)
+        kh = torch_ref.apply_rope(k, cosp, sinp, has_cls)
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            return F.scaled_dot_product_attention(qh, kh, v)
+
+    B, H, D, side, has_cls = wl["B"], wl["H"], wl["D"], wl["side"], wl["has_cls"]
+    N, C = side * side + int(has_cls), wl["H"] * wl["D"]
+    torch.manual_seed(0)
+    ours = RoPEAttention(C, H, H_img=side, has_cls=has_cls, device="cuda", dtype=torch.bfloat16)
+    ref = RoPEAttention(C, H, H_img=side, has_cls=has_cls, attn=torch_attn, device="cuda",
+                        dtype=torch.bfloat16)
+    ref.load_state_dict(ours.state_dict())
+    x = torch.randn(B, N, C, device="cuda", dtype=torch.bfloat16).requires_grad_(True)
+    dy = torch.randn(B, N, C, device="cuda", dtype=torch.bfloat16)
+    res = {}
+    for name, blk in (("ours", ours), ("torch", ref)):
+        def step():
+            x.grad = None
+            blk.zero_grad(set_to_none=True)
+            blk(x).backward(dy)
+
+        prewarm(step)
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        res[name] = (time.perf_counter() - t0) / steps * 1e3
+    return {"what": f"ViT attention sub-layer fwd+bwd, eager, bf16: x [{B},{N},{C}] -> qkv Linear -> "
+                    f"{H}-head 2D-RoPE attention -> proj; ours = RoPEAttention, torch = same layer with "
+                    "Python RoPE + torch SDPA (flash/efficient)",
+            "ours_ms": round(res["ours"], 4), "torch_ms": round(res["torch"], 4),
+            "speedup": round(res["torch"] / res["ours"], 3)}
+
+
 def profile_run(wl, steps, warmup):
     """Kernel launches only: `warmup + steps` x (fwd, bwd) and one calibration copy."""
     import torch
@@ -219,6 +268,9 @@ def main():
     ap.add_argument("--workload", default="vit_b", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-torch-baseline", action="store_true")
+    ap.add_argument("--block", action="store_true",
+                    help="also time the ViT attention sub-layer (qkv Linear -> op -> proj) against the "
+                         "same layer with torch SDPA + Python RoPE (reported as `vit_block`)")
     ap.add_argument("--profile", action="store_true",
                     help="profiling mode for rocprofv3: only the fwd/bwd ops (warmup + steps) and one "
                          "256 MiB device-to-device copy used to calibrate the HBM byte counters")
@@ -345,6 +397,8 @@ def main():
             result["torch_rocm"] = time_torch_rocm(wl, max(5, args.steps // 5), 3)
         except Exception as exc:  # reported, never fatal for the bench line
             result["torch_rocm"] = {"error": repr(exc)[:200]}
+    if args.block:
+        result["vit_block"] = time_block(wl, max(10, args.steps // 4), 3)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = time_cpu_baseline(wl)
     print(json.dumps(result), flush=True)

@@ -113,3 +113,37 @@ def test_custom_ops_registered_with_autograd():
     from torch._library.custom_ops import CustomOpDef
 
     assert isinstance(attention.attn_fwd, CustomOpDef)
+
+
+def test_rope_attention_block_passes_strided_views():
+    """The ViT block hands the op q/k/v as views of one qkv buffer (no copies)."""
+    from triton_fused_rope_flash_attn_amd import RoPEAttention
+
+    seen = {}
+
+    def spy(q, k, v, table, H_img=None, has_cls=True):
+        seen.update(shape=q.shape, strides=(q.stride(), k.stride(), v.stride()), H_img=H_img,
+                    has_cls=has_cls, base=q.untyped_storage().data_ptr(),
+                    offs=(q.storage_offset(), k.storage_offset(), v.storage_offset()),
+                    table=table.tables()[0].shape)
+        return q * 0
+
+    B, N, C, H = 2, 197, 384, 6
+    blk = RoPEAttention(C, H, H_img=14, has_cls=True, attn=spy, device="cpu")
+    out = blk(torch.randn(B, N, C))
+    D = C // H
+    assert out.shape == (B, N, C)
+    assert seen["shape"] == (B, H, N, D)
+    assert seen["strides"] == ((N * 3 * C, D, 3 * C, 1),) * 3
+    assert seen["offs"] == (0, C, 2 * C)
+    assert seen["H_img"] == 14 and seen["has_cls"] is True
+    assert seen["table"] == (196, D // 2)
+    assert {"rope.COSP", "rope.SINP"} <= set(blk.state_dict())
+
+
+def test_rope_attention_block_cpu_fails_loudly():
+    from triton_fused_rope_flash_attn_amd import RoPEAttention
+
+    blk = RoPEAttention(128, 2, H_img=4, has_cls=False, device="cpu")
+    with pytest.raises(RuntimeError, match="ROCm GPUs only"):
+        blk(torch.randn(1, 16, 128))

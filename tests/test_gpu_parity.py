@@ -297,3 +297,38 @@ def test_torch_compile_fullgraph():
     for name, a, b in zip(("O", "dQ", "dK", "dV"), *outs):
         _say(f"[compile] {name}: equal={torch.equal(a, b)}")
         assert torch.equal(a, b), name
+
+
+def test_vit_attention_block_matches_reference_block():
+    """RoPEAttention (qkv -> strided views -> fused op -> proj) vs the same block
+    and weights with the oracle attention (Python RoPE + fp32 math SDPA) in
+    its place: outputs and the gradients of x and both projections agree
+    to the op's tolerance (the linear layers are identical bf16 GEMMs)."""
+    from triton_fused_rope_flash_attn_amd import RoPEAttention
+
+    torch.manual_seed(0)
+    B, N, C, H = 8, 197, 384, 6
+
+    def oracle_attn(q, k, v, table, H_img=None, has_cls=True):
+        cosp, sinp = table.tables()
+        return torch_ref.attention(q.float(), k.float(), v.float(), cosp, sinp, has_cls).to(q.dtype)
+
+    ours = RoPEAttention(C, H, H_img=14, has_cls=True, device=DEV, dtype=torch.bfloat16)
+    ref = RoPEAttention(C, H, H_img=14, has_cls=True, attn=oracle_attn, device=DEV, dtype=torch.bfloat16)
+    ref.load_state_dict(ours.state_dict())
+    x = torch.randn(B, N, C, device=DEV, dtype=torch.bfloat16)
+    dy = torch.randn(B, N, C, device=DEV, dtype=torch.bfloat16)
+    res = []
+    for blk in (ours, ref):
+        xx = x.clone().requires_grad_(True)
+        y = blk(xx)
+        y.backward(dy)
+        torch.cuda.synchronize()
+        res.append((y.detach().float(), xx.grad.float(), blk.qkv.weight.grad.float(),
+                    blk.proj.weight.grad.float()))
+    for name, a, b in zip(("y", "dx", "dWqkv", "dWproj"), *res):
+        mx, mn = errors(a, b)
+        scale = b.abs().mean().item()
+        _say(f"[vit block] {name}: max {mx:.3e} mean {mn:.3e} (mean |ref| {scale:.3e})")
+        assert torch.isfinite(a).all(), name
+        assert mn <= 2e-2 * scale + 1e-3, name
