@@ -172,9 +172,9 @@ int farope_tile_config(const farope_attn_desc* desc, int32_t which, int32_t out[
   } else {
     const bool fu = bwd_fused(desc);
     out[0] = fu ? BWD_FUSED : BWD_SPLIT;
-    out[1] = fu ? bwd_fused_rows() : bwd_dkdv_block_rows(D);
+    out[1] = fu ? bwd_fused_rows() : bwd_dkdv_block_rows(D, desc->compute_dtype);
     out[2] = cdiv(N, out[1]);
-    out[3] = fu ? 512 : 256;
+    out[3] = fu ? 512 : bwd_dkdv_threads(D, desc->compute_dtype);
   }
   return FAROPE_OK;
 }
@@ -259,7 +259,7 @@ int farope_attn_bwd_dk_dv(const farope_attn_desc* desc, const void* q, const int
   p.vec_do = vec_ok(dout, dout_stride, es, desc->seq_len, desc->head_dim);
   p.vec_dk = vec_out_ok(dk, dk_stride, es, desc->seq_len, desc->head_dim);
   p.vec_dv = vec_out_ok(dv, dv_stride, es, desc->seq_len, desc->head_dim);
-  p.n_blk = cdiv(p.N, bwd_dkdv_block_rows(desc->head_dim));
+  p.n_blk = cdiv(p.N, bwd_dkdv_block_rows(desc->head_dim, desc->compute_dtype));
   return launch_rc(launch_bwd_dkdv(p, desc->io_dtype, desc->compute_dtype, desc->head_dim,
                                    static_cast<hipStream_t>(stream)));
 }
@@ -291,7 +291,7 @@ int farope_attn_bwd_dq(const farope_attn_desc* desc, const void* q, const int64_
   p.vec_v = vec_ok(v, v_stride, es, desc->seq_len, desc->head_dim);
   p.vec_do = vec_ok(dout, dout_stride, es, desc->seq_len, desc->head_dim);
   p.vec_dq = vec_out_ok(dq, dq_stride, es, desc->seq_len, desc->head_dim);
-  p.n_blk = cdiv(p.N, bwd_dq_block_rows(desc->head_dim));
+  p.n_blk = cdiv(p.N, bwd_dq_block_rows(desc->head_dim, desc->compute_dtype));
   return launch_rc(launch_bwd_dq(p, desc->io_dtype, desc->compute_dtype, desc->head_dim, false,
                                  static_cast<hipStream_t>(stream)));
 }
@@ -342,9 +342,9 @@ int farope_attn_bwd(const farope_attn_desc* desc, const void* q, const int64_t q
     p.n_blk = 1;
     return launch_rc(launch_bwd_fused(p, desc->io_dtype, desc->compute_dtype, st));
   }
-  p.n_blk = cdiv(p.N, bwd_dq_block_rows(D));
+  p.n_blk = cdiv(p.N, bwd_dq_block_rows(D, desc->compute_dtype));
   FAROPE_TRY(launch_rc(launch_bwd_dq(p, desc->io_dtype, desc->compute_dtype, D, true, st)));
-  p.n_blk = cdiv(p.N, bwd_dkdv_block_rows(D));
+  p.n_blk = cdiv(p.N, bwd_dkdv_block_rows(D, desc->compute_dtype));
   return launch_rc(launch_bwd_dkdv(p, desc->io_dtype, desc->compute_dtype, D, st));
 }
 

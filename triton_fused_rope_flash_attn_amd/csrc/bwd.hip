@@ -447,23 +447,46 @@ bwd_dkdv_kernel(const BwdParams p) {
 // ---------------------------------------------------------------------------
 // Tile table for the backward pass.
 // ---------------------------------------------------------------------------
-template <int D> struct BwdShape;
-template <> struct BwdShape<64> {
+// Rows per workgroup: the Q / dO (dK/dV kernel) and K / V (dQ kernel) rows
+// staged per workgroup are rotated and written to LDS once for all of its
+// waves, so wider workgroups amortise that staging over more keys / queries
+// (8 waves instead of 4: -29% at N = 1025, D = 128; two query subtiles per
+// dQ wave: another -13%).  fp32 compute splits every operand into two bf16
+// halves and needs the smaller tiles to fit its registers and LDS.
+template <int D, bool F32C> struct BwdShape;
+template <> struct BwdShape<64, false> {
+  static constexpr int DQ_NW = 8, DQ_QT = 2, DQ_KVS = 64;
+  static constexpr int KV_NW = 8, KV_KT = 2, KV_QS = 64;
+};
+template <> struct BwdShape<64, true> {
   static constexpr int DQ_NW = 4, DQ_QT = 2, DQ_KVS = 64;
   static constexpr int KV_NW = 4, KV_KT = 2, KV_QS = 64;
 };
-template <> struct BwdShape<128> {
-  static constexpr int DQ_NW = 4, DQ_QT = 1, DQ_KVS = 64;
-  static constexpr int KV_NW = 4, KV_KT = 1, KV_QS = 64;
+template <> struct BwdShape<128, false> {
+  static constexpr int DQ_NW = 8, DQ_QT = 2, DQ_KVS = 64;
+  static constexpr int KV_NW = 8, KV_KT = 1, KV_QS = 64;
+};
+template <> struct BwdShape<128, true> {
+  static constexpr int DQ_NW = 8, DQ_QT = 1, DQ_KVS = 64;
+  static constexpr int KV_NW = 8, KV_KT = 1, KV_QS = 64;
 };
 
-int bwd_dq_block_rows(int D) {
-  return D == 64 ? BwdShape<64>::DQ_NW * BwdShape<64>::DQ_QT * 16
-                 : BwdShape<128>::DQ_NW * BwdShape<128>::DQ_QT * 16;
+template <int D, bool F32C> static int dq_rows() { return BwdShape<D, F32C>::DQ_NW * BwdShape<D, F32C>::DQ_QT * 16; }
+template <int D, bool F32C> static int kv_rows() { return BwdShape<D, F32C>::KV_NW * BwdShape<D, F32C>::KV_KT * 16; }
+int bwd_dq_block_rows(int D, int ct) {
+  const bool f = ct == DT_F32;
+  return D == 64 ? (f ? dq_rows<64, true>() : dq_rows<64, false>())
+                 : (f ? dq_rows<128, true>() : dq_rows<128, false>());
 }
-int bwd_dkdv_block_rows(int D) {
-  return D == 64 ? BwdShape<64>::KV_NW * BwdShape<64>::KV_KT * 16
-                 : BwdShape<128>::KV_NW * BwdShape<128>::KV_KT * 16;
+int bwd_dkdv_block_rows(int D, int ct) {
+  const bool f = ct == DT_F32;
+  return D == 64 ? (f ? kv_rows<64, true>() : kv_rows<64, false>())
+                 : (f ? kv_rows<128, true>() : kv_rows<128, false>());
+}
+int bwd_dkdv_threads(int D, int ct) {
+  const bool f = ct == DT_F32;
+  return 64 * (D == 64 ? (f ? BwdShape<64, true>::KV_NW : BwdShape<64, false>::KV_NW)
+                       : (f ? BwdShape<128, true>::KV_NW : BwdShape<128, false>::KV_NW));
 }
 
 template <typename IO, int D>
@@ -492,7 +515,7 @@ hipError_t launch_bwd_pre(const BwdParams& p, int io, int D, hipStream_t st) {
 
 template <typename IO, int CT, int D>
 static hipError_t dq_launch(const BwdParams& p0, bool write_delta, hipStream_t st) {
-  using SH = BwdShape<D>;
+  using SH = BwdShape<D, CT == DT_F32>;
   BwdParams p = p0;
   const int grid = p.n_wg = p.B * p.H * p.n_blk;
   if (write_delta)
@@ -506,7 +529,7 @@ static hipError_t dq_launch(const BwdParams& p0, bool write_delta, hipStream_t s
 
 template <typename IO, int CT, int D>
 static hipError_t dkdv_launch(const BwdParams& p0, hipStream_t st) {
-  using SH = BwdShape<D>;
+  using SH = BwdShape<D, CT == DT_F32>;
   BwdParams p = p0;
   const int grid = p.n_wg = p.B * p.H * p.n_blk;
   hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS>), dim3(grid),

@@ -71,8 +71,9 @@ int persistent_grid(const void* kernel, int block_threads, int items, size_t dyn
 // Rows of q (fwd, dq) or kv (dk/dv) one work item / workgroup covers.
 int fwd_block_rows(int D);
 int fwd_threads(int D);
-int bwd_dq_block_rows(int D);
-int bwd_dkdv_block_rows(int D);
+int bwd_dq_block_rows(int D, int ct);
+int bwd_dkdv_block_rows(int D, int ct);
+int bwd_dkdv_threads(int D, int ct);
 int bwd_fused_rows();
 
 }  // namespace farope
