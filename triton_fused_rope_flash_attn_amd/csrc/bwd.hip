@@ -248,7 +248,12 @@ bwd_dq_kernel(const BwdParams p) {
 // ---------------------------------------------------------------------------
 // dK/dV kernel (KV-outer).
 // ---------------------------------------------------------------------------
-template <typename IO, int CT, int D, int NW, int KT, int QS>
+// VEC (Q and dO allow 16-byte access, decided on the host): the rows of the
+// next query stage are loaded into registers while the current stage is
+// computed, through buffer descriptors over the plane (rows >= N read 0), and
+// committed to LDS after the stage barrier.  Otherwise each stage is loaded
+// element-wise and synchronously.
+template <typename IO, int CT, int D, int NW, int KT, int QS, bool VEC>
 __global__ void __launch_bounds__(NW * 64)
 bwd_dkdv_kernel(const BwdParams p) {
   using C = Comp<CT>;
@@ -321,9 +326,78 @@ bwd_dkdv_kernel(const BwdParams p) {
 #pragma unroll
     for (int d = 0; d < DT; ++d) dvacc[u][d] = dkacc[u][d] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // ---- VEC: stage prefetch registers (thread t: row t / CPR, channels
+  //      8 (t % CPR) .. +7 of Q and dO, their table row; threads t < QS: LSE
+  //      and delta of row t) ----
+  constexpr unsigned ES = sizeof(IO);
+  static_assert(!VEC || (QS * CPR) % NT == 0, "every thread stages whole units");
+  static_assert(!VEC || QS <= NT, "one thread per staged LSE / delta");
+  Raw8<IO> pq[VEC ? ITER : 1], pg[VEC ? ITER : 1];
+  f32x4 pt[VEC ? ITER : 1][2];
+  float pl = 0.f, pd = 0.f;
+  auto prefetch = [&](int qb) __attribute__((always_inline)) {
+    if constexpr (VEC) {
+      const auto rQ = make_rsrc(Q, (unsigned)(((int64_t)(N - 1) * p.sq[2] + D) * ES));
+      const auto rG = make_rsrc(G, (unsigned)(((int64_t)(N - 1) * p.sdo[2] + D) * ES));
+#pragma unroll
+      for (int it = 0; it < ITER; ++it) {
+        const int c = tid + it * NT;
+        const int r = c / CPR, cc = c - r * CPR;
+        pq[it] = buf_load8<IO>(rQ, (unsigned)((r * (int)p.sq[2] + 8 * cc) * (int)ES),
+                               (unsigned)(qb * (int)p.sq[2] * (int)ES));
+        pg[it] = buf_load8<IO>(rG, (unsigned)((r * (int)p.sdo[2] + 8 * cc) * (int)ES),
+                               (unsigned)(qb * (int)p.sdo[2] * (int)ES));
+        // rows >= N are zero; any table row serves them
+        const f32x4* t = reinterpret_cast<const f32x4*>(tab + ((int64_t)(min(qb + r, N - 1) + shift) * D2 + 4 * cc) * 2);
+        pt[it][0] = t[0];
+        pt[it][1] = t[1];
+      }
+      if (tid < QS) {   // wave-uniform (QS is a multiple of 64)
+        const auto rl = make_rsrc(p.lse + prow, (unsigned)N * 4u);
+        const auto rd = make_rsrc(p.delta + prow, (unsigned)N * 4u);
+        pl = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rl, (unsigned)tid * 4u, (unsigned)qb * 4u, 0));
+        pd = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rd, (unsigned)tid * 4u, (unsigned)qb * 4u, 0));
+      }
+    }
+  };
+  auto commit = [&](int qb) __attribute__((always_inline)) {
+    if constexpr (VEC) {
+#pragma unroll
+      for (int it = 0; it < ITER; ++it) {
+        const int c = tid + it * NT;
+        const int r = c / CPR, cc = c - r * CPR;
+        float xq[8], xg[8];
+        unpack8(pq[it], xq);
+        unpack8(pg[it], xg);
+        const float cs[8] = {pt[it][0][0], pt[it][0][1], pt[it][0][2], pt[it][0][3],
+                             pt[it][1][0], pt[it][1][1], pt[it][1][2], pt[it][1][3]};
+        rope_rotate8(xq, cs);
+        C::put8(&sQ[r * LDQ + 8 * cc], xq);
+        C::put8(&sG[r * LDQ + 8 * cc], xg);
+        if constexpr (!TR) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            C::put1(&sQt[(8 * cc + e) * LDT + r], xq[e]);
+            C::put1(&sGt[(8 * cc + e) * LDT + r], xg[e]);
+          }
+        }
+      }
+      if (tid < QS) {
+        sL2[tid] = qb + tid < N ? pl * kLog2e : INFINITY;
+        sDl[tid] = qb + tid < N ? pd : 0.f;
+      }
+    }
+  };
+
+  prefetch(0);
   for (int qb = 0; qb < N; qb += QS) {
     const int rows = min(QS, round_up32(N - qb));
     lds_barrier();
+    if constexpr (VEC) {
+      commit(qb);
+      lds_barrier();
+      prefetch(qb + QS);   // past the last stage: rows >= N, read as 0
+    } else {
     // ---- stage Q-hat, Q-hat^T, dO, dO^T (+ delta, LSE) for this q stage ----
     {
       float xq[ITER][8], xg[ITER][8], cs[ITER][8];
@@ -364,6 +438,7 @@ bwd_dkdv_kernel(const BwdParams p) {
       }
     }
     lds_barrier();
+    }
 
     for (int j = 0; j < rows / 32; ++j) {
       float l2[8], dl[8];
@@ -532,8 +607,13 @@ static hipError_t dkdv_launch(const BwdParams& p0, hipStream_t st) {
   using SH = BwdShape<D, CT == DT_F32>;
   BwdParams p = p0;
   const int grid = p.n_wg = p.B * p.H * p.n_blk;
-  hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS>), dim3(grid),
-                     dim3(SH::KV_NW * 64), 0, st, p);
+  // (fp32 compute has no registers to spare for the prefetch)
+  if (CT != DT_F32 && p.vec_q && p.vec_do)
+    hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS, true>), dim3(grid),
+                       dim3(SH::KV_NW * 64), 0, st, p);
+  else
+    hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS, false>), dim3(grid),
+                       dim3(SH::KV_NW * 64), 0, st, p);
   return hipGetLastError();
 }
 
