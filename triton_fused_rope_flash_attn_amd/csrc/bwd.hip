@@ -20,6 +20,8 @@
 //    dS^T lands in the B-operand layout of dQ-hat^T += K-hat^T dS^T.  It
 //    can produce delta itself, so the split path needs no separate
 //    preprocessing launch.
+#include <type_traits>
+
 #include "common.h"
 #include "params.h"
 
@@ -56,7 +58,11 @@ __global__ void __launch_bounds__(256) bwd_pre_kernel(const BwdParams p) {
 // ---------------------------------------------------------------------------
 // dQ kernel (Q-outer).
 // ---------------------------------------------------------------------------
-template <typename IO, int CT, int D, int NW, int QT, int KVS, bool WRITE_DELTA>
+// VEC (K and V allow 16-byte access): the next KV block's raw rows are loaded
+// into registers while the current block is computed (buffer descriptors over
+// the plane, rows >= N read 0); their table rows are read when the block is
+// committed.  Otherwise each block is loaded synchronously.
+template <typename IO, int CT, int D, int NW, int QT, int KVS, bool WRITE_DELTA, bool VEC>
 __global__ void __launch_bounds__(NW * 64)
 bwd_dq_kernel(const BwdParams p) {
   using C = Comp<CT>;
@@ -143,9 +149,62 @@ bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
     for (int d = 0; d < DT; ++d) dqacc[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // ---- VEC: KV block prefetch registers (thread t: row t / CPR, channels
+  //      8 (t % CPR) .. +7 of K and V) ----
+  constexpr unsigned ES = sizeof(IO);
+  static_assert(!VEC || (KVS * CPR) % NT == 0, "every thread stages whole units");
+  Raw8<IO> pk[VEC ? ITER : 1], pv[VEC ? ITER : 1];
+  auto prefetch = [&](int kvb) __attribute__((always_inline)) {
+    if constexpr (VEC) {
+      const auto rK = make_rsrc(K, (unsigned)(((int64_t)(N - 1) * p.sk[2] + D) * ES));
+      const auto rV = make_rsrc(V, (unsigned)(((int64_t)(N - 1) * p.sv[2] + D) * ES));
+#pragma unroll
+      for (int it = 0; it < ITER; ++it) {
+        const int c = tid + it * NT;
+        const int r = c / CPR, cc = c - r * CPR;
+        pk[it] = buf_load8<IO>(rK, (unsigned)((r * (int)p.sk[2] + 8 * cc) * (int)ES),
+                               (unsigned)(kvb * (int)p.sk[2] * (int)ES));
+        pv[it] = buf_load8<IO>(rV, (unsigned)((r * (int)p.sv[2] + 8 * cc) * (int)ES),
+                               (unsigned)(kvb * (int)p.sv[2] * (int)ES));
+      }
+    }
+  };
+  auto commit = [&](int kvb) __attribute__((always_inline)) {
+    if constexpr (VEC) {
+#pragma unroll
+      for (int it = 0; it < ITER; ++it) {
+        const int c = tid + it * NT;
+        const int r = c / CPR, cc = c - r * CPR;
+        float xk[8], cs[8];
+        unpack8(pk[it], xk);
+        rope_load4(tab, min(kvb + r, N - 1) + shift, D2, 4 * cc, cs);   // rows >= N are zero
+        rope_rotate8(xk, cs);
+        C::put8(&sK[r * LDK + 8 * cc], xk);
+        if constexpr (std::is_same<IO, S>::value) {
+          *reinterpret_cast<typename Raw8<IO>::vec*>(&sV[r * LDK + 8 * cc]) = pv[it].v;
+        } else {
+          float xv[8];
+          unpack8(pv[it], xv);
+          C::put8(&sV[r * LDK + 8 * cc], xv);
+        }
+        if constexpr (!TR) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) C::put1(&sKt[(8 * cc + e) * LDT + r], xk[e]);
+        }
+      }
+    }
+  };
+
+  prefetch(0);
   for (int kvb = 0; kvb < N; kvb += KVS) {
     const int rows = min(KVS, round_up32(N - kvb));
     if (kvb > 0) lds_barrier();
+    if constexpr (VEC) {
+      commit(kvb);
+      lds_barrier();
+      prefetch(kvb + KVS);   // past the last block: rows >= N, read as 0
+      if (!wave_active) continue;
+    } else {
     {
       float xk[ITER][8], xv[ITER][8], cs[ITER][8];
 #pragma unroll
@@ -178,6 +237,7 @@ bwd_dq_kernel(const BwdParams p) {
     }
     lds_barrier();
     if (!wave_active) continue;
+    }
 
     for (int j = 0; j < rows / 32; ++j) {
       f32x4 sacc[QT][2], pacc[QT][2];
@@ -593,11 +653,23 @@ static hipError_t dq_launch(const BwdParams& p0, bool write_delta, hipStream_t s
   using SH = BwdShape<D, CT == DT_F32>;
   BwdParams p = p0;
   const int grid = p.n_wg = p.B * p.H * p.n_blk;
+  // (fp32 compute has no registers to spare for the prefetch)
+  if constexpr (CT != DT_F32) {
+    if (p.vec_k && p.vec_v) {
+      if (write_delta)
+        hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, true, true>),
+                           dim3(grid), dim3(SH::DQ_NW * 64), 0, st, p);
+      else
+        hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, false, true>),
+                           dim3(grid), dim3(SH::DQ_NW * 64), 0, st, p);
+      return hipGetLastError();
+    }
+  }
   if (write_delta)
-    hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, true>),
+    hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, true, false>),
                        dim3(grid), dim3(SH::DQ_NW * 64), 0, st, p);
   else
-    hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, false>),
+    hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, false, false>),
                        dim3(grid), dim3(SH::DQ_NW * 64), 0, st, p);
   return hipGetLastError();
 }
@@ -608,12 +680,15 @@ static hipError_t dkdv_launch(const BwdParams& p0, hipStream_t st) {
   BwdParams p = p0;
   const int grid = p.n_wg = p.B * p.H * p.n_blk;
   // (fp32 compute has no registers to spare for the prefetch)
-  if (CT != DT_F32 && p.vec_q && p.vec_do)
-    hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS, true>), dim3(grid),
-                       dim3(SH::KV_NW * 64), 0, st, p);
-  else
-    hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS, false>), dim3(grid),
-                       dim3(SH::KV_NW * 64), 0, st, p);
+  if constexpr (CT != DT_F32) {
+    if (p.vec_q && p.vec_do) {
+      hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS, true>), dim3(grid),
+                         dim3(SH::KV_NW * 64), 0, st, p);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS, false>), dim3(grid),
+                     dim3(SH::KV_NW * 64), 0, st, p);
   return hipGetLastError();
 }
 
