@@ -154,6 +154,9 @@ bwd_dq_kernel(const BwdParams p) {
   constexpr unsigned ES = sizeof(IO);
   static_assert(!VEC || (KVS * CPR) % NT == 0, "every thread stages whole units");
   Raw8<IO> pk[VEC ? ITER : 1], pv[VEC ? ITER : 1];
+  // with one unit per thread the table rows are prefetched too
+  constexpr bool TABPF = VEC && ITER == 1;
+  f32x4 pt[2];
   auto prefetch = [&](int kvb) __attribute__((always_inline)) {
     if constexpr (VEC) {
       const auto rK = make_rsrc(K, (unsigned)(((int64_t)(N - 1) * p.sk[2] + D) * ES));
@@ -166,6 +169,11 @@ bwd_dq_kernel(const BwdParams p) {
                                (unsigned)(kvb * (int)p.sk[2] * (int)ES));
         pv[it] = buf_load8<IO>(rV, (unsigned)((r * (int)p.sv[2] + 8 * cc) * (int)ES),
                                (unsigned)(kvb * (int)p.sv[2] * (int)ES));
+        if constexpr (TABPF) {
+          const f32x4* t = reinterpret_cast<const f32x4*>(tab + ((int64_t)(min(kvb + r, N - 1) + shift) * D2 + 4 * cc) * 2);
+          pt[0] = t[0];
+          pt[1] = t[1];
+        }
       }
     }
   };
@@ -177,7 +185,12 @@ bwd_dq_kernel(const BwdParams p) {
         const int r = c / CPR, cc = c - r * CPR;
         float xk[8], cs[8];
         unpack8(pk[it], xk);
-        rope_load4(tab, min(kvb + r, N - 1) + shift, D2, 4 * cc, cs);   // rows >= N are zero
+        if constexpr (TABPF) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) { cs[e] = pt[0][e]; cs[4 + e] = pt[1][e]; }
+        } else {
+          rope_load4(tab, min(kvb + r, N - 1) + shift, D2, 4 * cc, cs);   // rows >= N are zero
+        }
         rope_rotate8(xk, cs);
         C::put8(&sK[r * LDK + 8 * cc], xk);
         if constexpr (std::is_same<IO, S>::value) {
