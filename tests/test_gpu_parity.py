@@ -195,6 +195,38 @@ def test_channel_strided_inputs_generic_path():
     _compare("d-strided", ours, ref, out_dtype=torch.bfloat16)
 
 
+@pytest.mark.parametrize(
+    "side,has_cls,D,mode",
+    [(14, True, 128, "d-strided"), (16, True, 64, "d-strided"), (14, True, 128, "autocast"),
+     (16, True, 64, "autocast"), (14, True, 128, "fp16"), (16, True, 64, "fp32")],
+)
+def test_split_backward_io_variants(side, has_cls, D, mode):
+    """The split backward (N > 256 or D = 128) with generic-stride inputs (element-wise
+    staging), fp32 leaves under bf16 autocast (32-bit prefetch rows), fp16 I/O and fp32
+    compute (the 4-wave tiles)."""
+    N = side * side + int(has_cls)
+    B, H = 2, 3
+    g = torch.Generator().manual_seed(7)
+    dtype = {"fp16": torch.float16, "fp32": torch.float32, "autocast": torch.float32}.get(mode, torch.bfloat16)
+    if mode == "d-strided":
+        q, k, v = (torch.randn(B, H, D, N, generator=g).to(dtype).to(DEV).transpose(-1, -2) for _ in range(3))
+        assert q.stride(-1) != 1
+    else:
+        q, k, v = (torch.randn(B, H, N, D, generator=g).to(dtype).to(DEV) for _ in range(3))
+    do = torch.randn(B, H, N, D, generator=g).to(dtype).to(DEV)
+    table = CosSinTable(ROPE_BASE, side, D, device=DEV)
+    ours = _run_ours(q, k, v, do, table, has_cls,
+                     autocast_dtype=torch.bfloat16 if mode == "autocast" else None)
+    ref = _ref(q, k, v, do, table, has_cls)
+    tag = f"split-{mode}-N{N}-D{D}"
+    if mode == "fp32":
+        _compare(tag, ours, ref, tol_max=1e-4, tol_mean=1e-5)
+    elif mode == "autocast":
+        _compare(tag, ours, ref)
+    else:
+        _compare(tag, ours, ref, out_dtype=dtype)
+
+
 def test_stride0_dout_from_sum():
     cfg = dict(CONFIGS["vit_b"], B=4)
     q, k, v, _ = make_inputs(cfg, DEV)
