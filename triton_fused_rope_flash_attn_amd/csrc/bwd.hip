@@ -20,6 +20,10 @@
 //    dS^T lands in the B-operand layout of dQ-hat^T += K-hat^T dS^T.  It
 //    can produce delta itself, so the split path needs no separate
 //    preprocessing launch.
+//  * Both kernels restage (load, rotate, write to LDS) the rows of the
+//    other side of the plane for every workgroup, so workgroups are 8 waves
+//    wide (BwdShape), and with vector-accessible inputs the next stage's raw
+//    rows are prefetched into registers while the current one is computed.
 #include <type_traits>
 
 #include "common.h"
