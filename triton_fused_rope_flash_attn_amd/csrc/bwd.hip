@@ -606,6 +606,14 @@ bwd_dkdv_kernel(const BwdParams p) {
 // dQ wave: another -13%).  fp32 compute splits every operand into two bf16
 // halves and needs the smaller tiles to fit its registers and LDS.
 template <int D, bool F32C> struct BwdShape;
+template <> struct BwdShape<32, false> {
+  static constexpr int DQ_NW = 4, DQ_QT = 2, DQ_KVS = 64;
+  static constexpr int KV_NW = 4, KV_KT = 2, KV_QS = 64;
+};
+template <> struct BwdShape<32, true> {
+  static constexpr int DQ_NW = 4, DQ_QT = 2, DQ_KVS = 64;
+  static constexpr int KV_NW = 4, KV_KT = 2, KV_QS = 64;
+};
 template <> struct BwdShape<64, false> {
   static constexpr int DQ_NW = 8, DQ_QT = 2, DQ_KVS = 64;
   static constexpr int KV_NW = 8, KV_KT = 2, KV_QS = 64;
@@ -627,16 +635,19 @@ template <int D, bool F32C> static int dq_rows() { return BwdShape<D, F32C>::DQ_
 template <int D, bool F32C> static int kv_rows() { return BwdShape<D, F32C>::KV_NW * BwdShape<D, F32C>::KV_KT * 16; }
 int bwd_dq_block_rows(int D, int ct) {
   const bool f = ct == DT_F32;
+  if (D == 32) return f ? dq_rows<32, true>() : dq_rows<32, false>();
   return D == 64 ? (f ? dq_rows<64, true>() : dq_rows<64, false>())
                  : (f ? dq_rows<128, true>() : dq_rows<128, false>());
 }
 int bwd_dkdv_block_rows(int D, int ct) {
   const bool f = ct == DT_F32;
+  if (D == 32) return f ? kv_rows<32, true>() : kv_rows<32, false>();
   return D == 64 ? (f ? kv_rows<64, true>() : kv_rows<64, false>())
                  : (f ? kv_rows<128, true>() : kv_rows<128, false>());
 }
 int bwd_dkdv_threads(int D, int ct) {
   const bool f = ct == DT_F32;
+  if (D == 32) return 64 * (f ? BwdShape<32, true>::KV_NW : BwdShape<32, false>::KV_NW);
   return 64 * (D == 64 ? (f ? BwdShape<64, true>::KV_NW : BwdShape<64, false>::KV_NW)
                        : (f ? BwdShape<128, true>::KV_NW : BwdShape<128, false>::KV_NW));
 }
@@ -651,6 +662,13 @@ static hipError_t pre_io(const BwdParams& p, hipStream_t st) {
 }
 
 hipError_t launch_bwd_pre(const BwdParams& p, int io, int D, hipStream_t st) {
+  if (D == 32) {
+    switch (io) {
+      case DT_BF16: return pre_io<bf16, 32>(p, st);
+      case DT_F16: return pre_io<f16, 32>(p, st);
+      default: return pre_io<float, 32>(p, st);
+    }
+  }
   if (D == 64) {
     switch (io) {
       case DT_BF16: return pre_io<bf16, 64>(p, st);
@@ -727,7 +745,11 @@ static hipError_t dq_io(const BwdParams& p, int io, int ct, bool wd, hipStream_t
 }
 hipError_t launch_bwd_dq(const BwdParams& p, int io, int ct, int D, bool write_delta,
                          hipStream_t st) {
-  return D == 64 ? dq_io<64>(p, io, ct, write_delta, st) : dq_io<128>(p, io, ct, write_delta, st);
+  switch (D) {
+    case 32: return dq_io<32>(p, io, ct, write_delta, st);
+    case 64: return dq_io<64>(p, io, ct, write_delta, st);
+    default: return dq_io<128>(p, io, ct, write_delta, st);
+  }
 }
 
 template <typename IO, int D>
@@ -747,7 +769,11 @@ static hipError_t kv_io(const BwdParams& p, int io, int ct, hipStream_t st) {
   }
 }
 hipError_t launch_bwd_dkdv(const BwdParams& p, int io, int ct, int D, hipStream_t st) {
-  return D == 64 ? kv_io<64>(p, io, ct, st) : kv_io<128>(p, io, ct, st);
+  switch (D) {
+    case 32: return kv_io<32>(p, io, ct, st);
+    case 64: return kv_io<64>(p, io, ct, st);
+    default: return kv_io<128>(p, io, ct, st);
+  }
 }
 
 // ---------------------------------------------------------------------------

@@ -787,13 +787,17 @@ fwd_kernel(const FwdParams p) {
 // TABROWS: rows of the packed RoPE table an LDS-resident copy can hold
 // (N + 1 - has_cls <= TABROWS; i.e. planes up to 256 tokens).
 template <int D> struct FwdShape;
+template <> struct FwdShape<32> { static constexpr int NW = 8, QT = 2, KC = 128, TABROWS = 257; };
 template <> struct FwdShape<64> { static constexpr int NW = 8, QT = 2, KC = 128, TABROWS = 257; };
 template <> struct FwdShape<128> { static constexpr int NW = 8, QT = 1, KC = 64, TABROWS = 0; };
 
+template <int D> static int fwd_rows() { return FwdShape<D>::NW * FwdShape<D>::QT * 16; }
 int fwd_block_rows(int D) {
-  return D == 64 ? FwdShape<64>::NW * FwdShape<64>::QT * 16 : FwdShape<128>::NW * FwdShape<128>::QT * 16;
+  return D == 32 ? fwd_rows<32>() : D == 64 ? fwd_rows<64>() : fwd_rows<128>();
 }
-int fwd_threads(int D) { return D == 64 ? FwdShape<64>::NW * 64 : FwdShape<128>::NW * 64; }
+int fwd_threads(int D) {
+  return 64 * (D == 32 ? FwdShape<32>::NW : D == 64 ? FwdShape<64>::NW : FwdShape<128>::NW);
+}
 
 template <typename IO, int CT, int D>
 static hipError_t fwd_launch(const FwdParams& p0, hipStream_t st) {
@@ -816,7 +820,11 @@ static hipError_t fwd_launch(const FwdParams& p0, hipStream_t st) {
 
 template <typename IO, int CT>
 static hipError_t fwd_shape(const FwdParams& p, int D, hipStream_t st) {
-  return D == 64 ? fwd_launch<IO, CT, 64>(p, st) : fwd_launch<IO, CT, 128>(p, st);
+  switch (D) {
+    case 32: return fwd_launch<IO, CT, 32>(p, st);
+    case 64: return fwd_launch<IO, CT, 64>(p, st);
+    default: return fwd_launch<IO, CT, 128>(p, st);
+  }
 }
 
 template <typename IO>
