@@ -257,10 +257,23 @@ bwd_dq_kernel(const BwdParams p) {
     }
 
     for (int j = 0; j < rows / 32; ++j) {
+      // The logit accumulators (rows = keys kbase + 4h + i of this lane) start
+      // at 0 for keys < N and -inf beyond, so P = exp2(S*c - LSE2) is 0 there
+      // with no per-element select; the dP accumulators start at -delta of the
+      // lane's query, so dP - delta needs no subtraction.
+      const int kbase = kvb + 32 * j + 8 * lg;
+      f32x4 kmask[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kmask[h][i] = kbase + 4 * h + i < N ? 0.f : -INFINITY;
       f32x4 sacc[QT][2], pacc[QT][2];
 #pragma unroll
-      for (int t = 0; t < QT; ++t)
-        sacc[t][0] = sacc[t][1] = pacc[t][0] = pacc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int t = 0; t < QT; ++t) {
+        sacc[t][0] = kmask[0];
+        sacc[t][1] = kmask[1];
+        pacc[t][0] = pacc[t][1] = f32x4{-dlt[t], -dlt[t], -dlt[t], -dlt[t]};
+      }
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
 #pragma unroll
@@ -275,8 +288,6 @@ bwd_dq_kernel(const BwdParams p) {
           }
         }
       }
-      const int kbase = kvb + 32 * j + 8 * lg;
-      const bool full = kvb + 32 * j + 32 <= N;
       Frag dsf[QT];
 #pragma unroll
       for (int t = 0; t < QT; ++t) {
@@ -284,11 +295,8 @@ bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const bool valid = full || kbase + 4 * h + i < N;
-            const float pr = valid ? fast_exp2(sacc[t][h][i] * p.scale_log2 - lse2[t]) : 0.f;
-            ds[4 * h + i] = pr * (pacc[t][h][i] - dlt[t]);
-          }
+          for (int i = 0; i < 4; ++i)
+            ds[4 * h + i] = fast_exp2(__builtin_fmaf(sacc[t][h][i], p.scale_log2, -lse2[t])) * pacc[t][h][i];
         dsf[t] = C::make(ds);
       }
 #pragma unroll
