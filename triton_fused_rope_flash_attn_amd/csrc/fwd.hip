@@ -468,9 +468,11 @@ fwd_kernel(const FwdParams p) {
   };
   // One KV chunk of nb blocks; the block holding key N-1 is the last one of
   // the chunk that starts at kvb (the ragged chunk is processed first).
-  auto chunk = [&](const S* __restrict__ cK, const S* __restrict__ cV, int kvb) __attribute__((always_inline)) {
+  auto chunk = [&](const S* __restrict__ cK, const S* __restrict__ cV, int kvb, bool active, auto&& mem) __attribute__((always_inline)) {
     const int nkeys = min(KC, N - kvb);
-    const int nb = (nkeys + 31) >> 5;
+    // a wave with no query row below N runs one block (its results are never
+    // stored) so that every wave reaches mem() on the same straight-line path
+    const int nb = active ? (nkeys + 31) >> 5 : 1;
     SAcc s0, s1;
     KFr ka, kb;
     VFr vf;
@@ -478,6 +480,11 @@ fwd_kernel(const FwdParams p) {
     load_k(cK, 0, ka);
     logits(ka, s0);
     load_k(cK, min(1, nb - 1), kb);
+    // The chunk's prefetch loads issue here, under the first block's
+    // products, rather than in a burst before the barrier.
+    __builtin_amdgcn_sched_barrier(0);
+    mem();
+    __builtin_amdgcn_sched_barrier(0);
     // Step j: the logits of block j+1 (its K-hat is already in registers) go
     // to the MFMA pipe first and run under block j's softmax; block j+2's
     // K-hat (into the registers block j's K-hat has left) and block j's V^T
@@ -690,23 +697,34 @@ fwd_kernel(const FwdParams p) {
       constexpr bool FIRST = decltype(firstc)::value;
       const int slot = g & 1;
       commit_kv(slot, chunk_start(c));
-      if constexpr (FIRST) {
-        flush_o();
-        // the next item's Q rows before the next KV chunk: Q is waited for
-        // first, at the next item's start, so at least one KV load is younger
-        // and stays in flight across that wait (also when nch == 1)
-        prefetch_q(nxt >= 0 ? nxt : item);
-      }
-      const bool last = c + 1 == nch;
-      const int tgt = last ? (nxt >= 0 ? nxt : item) : item;
-      if (last) kvr = kv_rs(tgt);
-      prefetch_kv(tgt, kvr, last ? 0 : c + 1);
-      lds_barrier();
-      if (nt > 0) {
-        if constexpr (kPipe)
-          chunk(sK[slot], sVt[slot], chunk_start(c));
-        else
-          chunk_serial(sK[slot], sVt[slot], chunk_start(c));
+      if constexpr (FIRST && kPipe) flush_o();
+      auto mem = [&]() __attribute__((always_inline)) {
+        if constexpr (FIRST) {
+          if constexpr (!kPipe) flush_o();
+          // the next item's Q rows before the next KV chunk: Q is waited for
+          // first, at the next item's start, so at least one KV load is younger
+          // and stays in flight across that wait (also when nch == 1)
+          prefetch_q(nxt >= 0 ? nxt : item);
+        }
+        const bool last = c + 1 == nch;
+        const int tgt = last ? (nxt >= 0 ? nxt : item) : item;
+        if (last) kvr = kv_rs(tgt);
+        prefetch_kv(tgt, kvr, last ? 0 : c + 1);
+      };
+      // The O stores and the Q/KV prefetch of a chunk switch (~96 KB per
+      // workgroup at 64 channels) pass through the CU's vector memory path
+      // in over a thousand cycles, and a wave stalls at issue while that path
+      // is full.  Issued before the barrier, the loads hold every wave there;
+      // the pipelined chunk issues them after its first products instead, so
+      // they drain while the SIMDs compute.  (The stores stay before the
+      // barrier: issued under the products they stalled the first block.)
+      if constexpr (kPipe) {
+        lds_barrier();
+        chunk(sK[slot], sVt[slot], chunk_start(c), nt > 0, mem);
+      } else {
+        mem();
+        lds_barrier();
+        if (nt > 0) chunk_serial(sK[slot], sVt[slot], chunk_start(c));
       }
       ++g;
     };
