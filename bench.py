@@ -145,12 +145,27 @@ def time_cpu_baseline(wl, budget_s=12.0):
     }
 
 
+def torch_rope(x, cosp, sinp, has_cls):
+    """2D RoPE applied in plain torch ops, as the reference README's comparison
+    model does (README:125): channel pairs (2p, 2p+1) of token s rotate by
+    table row max(s - has_cls, 0), and a CLS token passes through.  This is
+    the torch-ROCm comparison's own RoPE, in the input dtype."""
+    import torch
+    N = x.shape[-2]
+    c, s = cosp.to(dtype=x.dtype), sinp.to(dtype=x.dtype)
+    if has_cls:   # an identity row (cos 1, sin 0) leaves the CLS token unchanged, exactly
+        c = torch.cat([torch.ones_like(c[:1]), c])
+        s = torch.cat([torch.zeros_like(s[:1]), s])
+    c, s = c[:N], s[:N]
+    xe, xo = x[..., 0::2], x[..., 1::2]
+    return torch.stack([xe * c - xo * s, xo * c + xe * s], dim=-1).flatten(-2)
+
+
 def time_torch_rocm(wl, steps, warmup):
     """Python 2D RoPE (bf16) + torch SDPA (flash/efficient backend) fwd+bwd on the GPU."""
     import torch
     import torch.nn.functional as F
     from torch.nn.attention import SDPBackend, sdpa_kernel
-    from oracle import torch_ref
     from triton_fused_rope_flash_attn_amd import CosSinTable
 
     q, k, v, do = make_inputs(wl, "cuda")
@@ -158,8 +173,8 @@ def time_torch_rocm(wl, steps, warmup):
     qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
 
     def step():
-        qh = torch_ref.apply_rope(qq, table.COSP, table.SINP, wl["has_cls"])
-        kh = torch_ref.apply_rope(kk, table.COSP, table.SINP, wl["has_cls"])
+        qh = torch_rope(qq, table.COSP, table.SINP, wl["has_cls"])
+        kh = torch_rope(kk, table.COSP, table.SINP, wl["has_cls"])
         with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
             o = F.scaled_dot_product_attention(qh, kh, vv)
         o.backward(do)
@@ -179,20 +194,26 @@ def time_torch_rocm(wl, steps, warmup):
             "what": "Python 2D RoPE (bf16) + F.scaled_dot_product_attention (flash/efficient), fwd+bwd"}
 
 
-def time_block(wl, steps, warmup):
-    """ViT attention sub-layer (qkv Linear -> op -> proj), eager fwd+bwd, bf16:
+def time_block(wl, steps, warmup, compiled=False):
+    """ViT attention sub-layer (qkv Linear -> op -> proj), fwd+bwd, bf16:
     ``RoPEAttention`` with the fused op vs the same layer and weights with
-    Python RoPE + torch SDPA (flash/efficient) in its place."""
+    Python RoPE + torch SDPA (flash/efficient) in its place.  ``compiled``:
+    both layers under ``torch.compile`` (Inductor), the setting of the
+    reference README's compiled comparison (README:165-195); the fused op stays
+    one opaque custom op inside the compiled graph."""
     import torch
     import torch.nn.functional as F
     from torch.nn.attention import SDPBackend, sdpa_kernel
-    from oracle import torch_ref
     from triton_fused_rope_flash_attn_amd import RoPEAttention
 
     def torch_attn(q, k, v, table, H_img=None, has_cls=True):
         cosp, sinp = table.tables()
-        qh = torch_ref.apply_rope(q, cosp, sinp, has_cls)
-        kh = torch_ref.apply_rope(k, cosp, sinp, has_cls)
+        qh = torch_rope(q, cosp, sinp, has_cls)
+        kh = torch_rope(k, cosp, sinp, has_cls)
+        if compiled:
+            # Inductor's stride check on torch's flash-attention backward
+            # rejects the strided V view of the qkv buffer; a copy avoids it
+            v = v.contiguous()
         with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
             return F.scaled_dot_product_attention(qh, kh, v)
 
@@ -207,10 +228,14 @@ def time_block(wl, steps, warmup):
     dy = torch.randn(B, N, C, device="cuda", dtype=torch.bfloat16)
     res = {}
     for name, blk in (("ours", ours), ("torch", ref)):
+        fwd = torch.compile(blk) if compiled else blk
+        if compiled:
+            print(f"bench.py: compiling the {name} layer (Inductor)", file=sys.stderr, flush=True)
+
         def step():
             x.grad = None
             blk.zero_grad(set_to_none=True)
-            blk(x).backward(dy)
+            fwd(x).backward(dy)
 
         prewarm(step)
         for _ in range(warmup):
@@ -221,7 +246,8 @@ def time_block(wl, steps, warmup):
             step()
         torch.cuda.synchronize()
         res[name] = (time.perf_counter() - t0) / steps * 1e3
-    return {"what": f"ViT attention sub-layer fwd+bwd, eager, bf16: x [{B},{N},{C}] -> qkv Linear -> "
+    return {"what": f"ViT attention sub-layer fwd+bwd, {'torch.compile (Inductor)' if compiled else 'eager'}, "
+                    f"bf16: x [{B},{N},{C}] -> qkv Linear -> "
                     f"{H}-head 2D-RoPE attention -> proj; ours = RoPEAttention, torch = same layer with "
                     "Python RoPE + torch SDPA (flash/efficient)",
             "ours_ms": round(res["ours"], 4), "torch_ms": round(res["torch"], 4),
@@ -271,6 +297,9 @@ def main():
     ap.add_argument("--block", action="store_true",
                     help="also time the ViT attention sub-layer (qkv Linear -> op -> proj) against the "
                          "same layer with torch SDPA + Python RoPE (reported as `vit_block`)")
+    ap.add_argument("--compile", action="store_true",
+                    help="with --block: also time both layers under torch.compile (Inductor), reported as "
+                         "`vit_block_compiled`")
     ap.add_argument("--profile", action="store_true",
                     help="profiling mode for rocprofv3: only the fwd/bwd ops (warmup + steps) and one "
                          "256 MiB device-to-device copy used to calibrate the HBM byte counters")
@@ -399,6 +428,8 @@ def main():
             result["torch_rocm"] = {"error": repr(exc)[:200]}
     if args.block:
         result["vit_block"] = time_block(wl, max(10, args.steps // 4), 3)
+        if args.compile:
+            result["vit_block_compiled"] = time_block(wl, max(10, args.steps // 4), 3, compiled=True)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = time_cpu_baseline(wl)
     print(json.dumps(result), flush=True)

@@ -147,3 +147,24 @@ def test_rope_attention_block_cpu_fails_loudly():
     blk = RoPEAttention(128, 2, H_img=4, has_cls=False, device="cpu")
     with pytest.raises(RuntimeError, match="ROCm GPUs only"):
         blk(torch.randn(1, 16, 128))
+
+
+@pytest.mark.parametrize("has_cls", [True, False])
+def test_bench_torch_rope_matches_oracle(has_cls):
+    """bench.py's torch-ROCm comparison applies its own Python RoPE; it must be
+    the oracle's rotation."""
+    import importlib.util
+    import pathlib
+
+    from oracle import torch_ref
+    from triton_fused_rope_flash_attn_amd import build_axial_rope_pairs
+
+    spec = importlib.util.spec_from_file_location("bench", pathlib.Path(__file__).parents[1] / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    side, D = 4, 32
+    N = side * side + int(has_cls)
+    cosp, sinp = build_axial_rope_pairs(side, D, torch.device("cpu"), base=100.0)
+    x = torch.randn(2, 3, N, D, generator=torch.Generator().manual_seed(1))
+    torch.testing.assert_close(bench.torch_rope(x, cosp, sinp, has_cls),
+                               torch_ref.apply_rope(x, cosp, sinp, has_cls), rtol=0, atol=0)
