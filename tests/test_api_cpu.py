@@ -168,3 +168,45 @@ def test_bench_torch_rope_matches_oracle(has_cls):
     x = torch.randn(2, 3, N, D, generator=torch.Generator().manual_seed(1))
     torch.testing.assert_close(bench.torch_rope(x, cosp, sinp, has_cls),
                                torch_ref.apply_rope(x, cosp, sinp, has_cls), rtol=0, atol=0)
+
+
+def test_packed_table_cache_invalidation(monkeypatch):
+    """CosSinTable.packed() repacks after load_state_dict (in place), buffer
+    reassignment, .data reassignment and in-place edits, and reuses the cache
+    otherwise; pickles and deep copies drop the cache (it is derived state).
+    The GPU packer is replaced by a counting stand-in."""
+    import copy
+    import pickle
+
+    from triton_fused_rope_flash_attn_amd import rope as rope_mod
+
+    calls = []
+
+    def fake_pack(c, s):
+        calls.append((c.clone(), s.clone()))
+        return torch.cat([c.flatten(), s.flatten()])
+
+    monkeypatch.setattr(rope_mod, "pack_rope_tables", fake_pack)
+    t = CosSinTable(100.0, 4, 16, device="cpu")
+    a = t.packed()
+    assert len(calls) == 1 and t.packed() is a and len(calls) == 1
+    other = CosSinTable(10000.0, 4, 16, device="cpu")
+    t.load_state_dict(other.state_dict())
+    b = t.packed()
+    assert len(calls) == 2 and torch.equal(calls[-1][0], other.COSP)
+    t.COSP = other.COSP.clone() * 0.5
+    t.packed()
+    assert len(calls) == 3 and torch.equal(calls[-1][0], other.COSP * 0.5)
+    t.SINP.data = torch.zeros_like(t.SINP)
+    t.packed()
+    assert len(calls) == 4 and torch.equal(calls[-1][1], torch.zeros_like(t.SINP))
+    t.COSP.mul_(2.0)
+    t.packed()
+    assert len(calls) == 5 and t.packed() is not b and len(calls) == 5
+    assert len(pickle.dumps(t)) > 0   # the weak references are not pickled
+    clone = copy.deepcopy(t)
+    assert clone._packed is None and clone._packed_key is None
+    assert torch.equal(clone.COSP, t.COSP)
+    n = len(calls)
+    clone.packed()
+    assert len(calls) == n + 1

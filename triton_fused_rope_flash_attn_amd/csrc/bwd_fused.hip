@@ -466,9 +466,12 @@ bwd_plane_kernel(const BwdParams p) {
   while (plane >= 0) {
     const int nxt = item_of(it + 1);
     const auto rdq = rsrc(p.dq, p.sdq, plane);   // (VEC)
-    // No barrier is needed before these writes: the previous plane's last
-    // reads of sQ / sG / sL2 / sDl (its last sweep) precede its tail barrier,
-    // and sK is only read right after the barrier below.
+    // The previous plane's last reads of sQ / sG / sL2 / sDl (its last sweep)
+    // precede its tail barrier, so these writes need no barrier of their own.
+    // sK is read by load_kq right after the barrier below (16-bit I/O), or,
+    // with 32-bit I/O, by every dQ product including the previous plane's
+    // tail dQ; that variant ends each plane with a barrier (see the loop end)
+    // so that no wave rewrites its sK rows while another still reads them.
     commit_kv();
     commit(0, 0);
     // sK and the first stage are complete, and every wave has finished the
@@ -590,6 +593,12 @@ bwd_plane_kernel(const BwdParams p) {
           }
         }
       }
+    }
+    // 32-bit I/O reads K-hat^T from sK in the tail dQ above: every wave must
+    // be past it before the next plane's commit_kv overwrites sK (the
+    // barrier orders LDS only, so the dK / dV stores stay in flight).
+    if constexpr (!KQREG) {
+      if (nxt >= 0) lds_barrier();   // nxt is workgroup-uniform
     }
     plane = nxt;
     ++it;

@@ -14,13 +14,14 @@ Same names, signatures, buffer names, shapes and values as the reference
 The kernels consume a derived table (``CosSinTable.packed()``): fp32
 ``[(n_pos + 1), D/2, 2]`` with (cos, sin) interleaved per pair and an
 identity row 0 for the CLS token.  It is built on the GPU by
-``farope_rope_pack`` and cached per (storage, version) of COSP/SINP, so an
-in-place update (e.g. ``load_state_dict``) rebuilds it; it is not part of
-``state_dict``.
+``farope_rope_pack`` and cached per COSP/SINP tensor object, version and
+storage, so an in-place update (e.g. ``load_state_dict``) or a reassigned
+buffer rebuilds it; it is not part of ``state_dict``.
 """
 from __future__ import annotations
 
 import math
+import weakref
 
 import torch
 
@@ -109,6 +110,14 @@ class CosSinTable(torch.nn.Module):
         """``(COSP, SINP)``, each ``[N_pos, D2]`` fp32 (FA:1161-1166)."""
         return self.COSP, self.SINP
 
+    def __getstate__(self):
+        # The packed-table cache (weak references included) is derived state:
+        # pickles and deep copies rebuild it on first use.
+        state = self.__dict__.copy()
+        state["_packed"] = None
+        state["_packed_key"] = None
+        return state
+
     @property
     def H_img(self) -> int:
         n_pos = self.COSP.shape[0]
@@ -118,7 +127,15 @@ class CosSinTable(torch.nn.Module):
         return side
 
     def packed(self) -> torch.Tensor:
-        """Kernel-layout table, rebuilt when COSP/SINP change (storage, version, device).
+        """Kernel-layout table, rebuilt whenever COSP/SINP may have changed.
+
+        The cache holds weak references to the COSP/SINP tensor objects it was
+        built from, with their version counters and storage pointers.  It is
+        rebuilt when either buffer is a different object (``table.COSP = t``,
+        ``.to()``, ``_apply``), was modified in place (``load_state_dict``,
+        ``copy_``: the version counter moves) or points at other storage
+        (``.data`` reassignment).  A new tensor that happens to reuse a freed
+        address is still a different object, so it cannot hit a stale entry.
 
         Under ``torch.compile`` the table is packed inside the graph on every call
         (one small kernel): the cache key reads storage pointers, which traced
@@ -127,8 +144,15 @@ class CosSinTable(torch.nn.Module):
         c, s = self.COSP, self.SINP
         if torch.compiler.is_compiling():
             return pack_rope_tables(c, s)
-        key = (c.data_ptr(), c._version, s.data_ptr(), s._version, c.device, tuple(c.shape))
-        if self._packed is None or self._packed_key != key:
+        key = self._packed_key
+        if (
+            self._packed is None
+            or key is None
+            or key[0]() is not c
+            or key[1]() is not s
+            or key[2:] != (c._version, s._version, c.data_ptr(), s.data_ptr())
+        ):
             self._packed = pack_rope_tables(c, s)
-            self._packed_key = key
+            self._packed_key = (weakref.ref(c), weakref.ref(s), c._version, s._version,
+                                c.data_ptr(), s.data_ptr())
         return self._packed
