@@ -41,8 +41,13 @@ typedef enum farope_status {
   FAROPE_ERR_TABLE = 5,       /* RoPE table geometry inconsistent with the call */
   FAROPE_ERR_SHAPE = 6,       /* batch/heads not positive or sizes overflow */
   FAROPE_ERR_LAUNCH = 7,      /* the HIP runtime rejected a kernel launch */
-  FAROPE_ERR_ALIGN = 8        /* a pointer is not aligned to its element size */
+  FAROPE_ERR_ALIGN = 8,       /* a pointer is not aligned to its element size */
+  FAROPE_ERR_SCRATCH = 9      /* batch*heads*seq_len > FAROPE_NOALLOC_MAX_ROWS (noalloc entry) */
 } farope_status;
+
+/* Rows (batch * heads * seq_len) the static workspace of
+ * farope_attn_bwd_noalloc holds: 4 Mi fp32 values = 16 MiB per device. */
+#define FAROPE_NOALLOC_MAX_ROWS 4194304
 
 /* Problem description shared by all attention entry points. */
 typedef struct farope_attn_desc {
@@ -138,6 +143,29 @@ int farope_attn_bwd(const farope_attn_desc* desc,
                     void* dk, const int64_t dk_stride[4],
                     void* dv, const int64_t dv_stride[4],
                     float* delta_ws, void* stream);
+
+/*
+ * farope_attn_bwd without the caller workspace: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops, harnesses that forbid hipMalloc).  The split
+ * path's delta rows live in a static device array of FAROPE_NOALLOC_MAX_ROWS
+ * fp32 values that the library holds on every device it runs on until the
+ * process ends; larger calls return FAROPE_ERR_SCRATCH before anything is
+ * launched.  Allocates nothing.  Calls on one device share that array, so
+ * calls that overlap on one device (concurrent streams or threads) race;
+ * calls ordered on one stream do not.  The current device must be the one
+ * holding the tensors.
+ */
+int farope_attn_bwd_noalloc(const farope_attn_desc* desc,
+                            const void* q, const int64_t q_stride[4],
+                            const void* k, const int64_t k_stride[4],
+                            const void* v, const int64_t v_stride[4],
+                            const void* o, const int64_t o_stride[4],
+                            const void* dout, const int64_t dout_stride[4],
+                            const float* lse, const float* rope_packed,
+                            void* dq, const int64_t dq_stride[4],
+                            void* dk, const int64_t dk_stride[4],
+                            void* dv, const int64_t dv_stride[4], void* stream);
 
 /*
  * Tile table query (replaces the reference's triton.autotune configs,

@@ -52,9 +52,9 @@ def test_desc_struct_layout():
 
 
 def test_strerror_covers_all_codes(lib):
-    texts = {rc: _lib.strerror(rc) for rc in range(0, 9)}
+    texts = {rc: _lib.strerror(rc) for rc in range(0, 10)}
     assert texts[0] == "success"
-    assert len(set(texts.values())) == 9
+    assert len(set(texts.values())) == 10
     assert "unknown" in _lib.strerror(1234)
 
 
@@ -127,3 +127,18 @@ def test_bwd_entry_points_reject_bad_arguments(lib):
     assert lib.farope_attn_bwd_dk_dv(ctypes.byref(good), *([16, s] * 4), 16, 16, 16, 16, s, None, s, None) == _lib.ERR_NULL
     assert lib.farope_rope_pack(16, 32, 1, 16, 32, 1, 196, 31, 16, None) == _lib.ERR_TABLE
     assert lib.farope_rope_pack(None, 32, 1, 16, 32, 1, 196, 32, 16, None) == _lib.ERR_NULL
+
+
+def test_noalloc_bwd_rejects_oversize_before_any_launch(lib):
+    """farope_attn_bwd_noalloc refuses calls whose B*H*N exceeds its static
+    workspace (FAROPE_NOALLOC_MAX_ROWS) with FAROPE_ERR_SCRATCH, on the host."""
+    m = re.search(r"#define FAROPE_NOALLOC_MAX_ROWS (\d+)", open(HEADER).read())
+    assert int(m.group(1)) == _lib.NOALLOC_MAX_ROWS
+    s = _lib.Stride4(0, 0, 0, 1)
+    N = 1025   # split path; 4096 planes x 1025 rows > 4 Mi rows
+    big = _lib.make_desc(64, 64, N, 128, N - 1, True, _lib.BF16, _lib.BF16, 128 ** -0.5)
+    assert 64 * 64 * N > _lib.NOALLOC_MAX_ROWS
+    assert lib.farope_attn_bwd_noalloc(ctypes.byref(big), *([16, s] * 5), 16, 16, *([16, s] * 3), None) == _lib.ERR_SCRATCH
+    bad = _lib.make_desc(2, 3, 197, 60, 196, True, _lib.BF16, _lib.BF16, 0.125)
+    assert lib.farope_attn_bwd_noalloc(ctypes.byref(bad), *([16, s] * 5), 16, 16, *([16, s] * 3), None) == _lib.ERR_HEAD_DIM
+    assert "static workspace" in _lib.strerror(_lib.ERR_SCRATCH)

@@ -1,0 +1,52 @@
+"""farope_attn_bwd_noalloc (static device workspace, no allocation) against
+farope_attn_bwd (caller workspace), both called through the C ABI.
+
+Two split-path calls in a row (N > 256, then a smaller D = 128 problem) and
+one one-pass call: the same kernels run with the delta rows in the library's
+static array instead of a caller buffer, so dQ, dK and dV must be identical
+bit for bit.  The second call reuses the array the first one left behind.
+"""
+from __future__ import annotations
+
+import math
+import sys
+
+import pytest
+import torch
+
+from tests.cases import ROPE_BASE, make_inputs
+from triton_fused_rope_flash_attn_amd import CosSinTable
+from triton_fused_rope_flash_attn_amd import _lib
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _one(B, H, side, has_cls, D, seed):
+    N = side * side + int(has_cls)
+    print(f"noalloc case B={B} H={H} N={N} D={D}", flush=True)
+    sys.stdout.flush()
+    cfg = dict(B=B, H=H, side=side, has_cls=has_cls, D=D, dtype=torch.bfloat16, scale=1.0, dout="randn")
+    q, k, v, do = make_inputs(cfg, DEV, seed=seed)
+    table = CosSinTable(ROPE_BASE, side, D, device=DEV)
+    rope = table.packed()
+    scale = 1.0 / math.sqrt(D)
+    n_pos = side * side
+    o, lse = torch.ops.farope.attn_fwd(q, k, v, rope, n_pos, has_cls, scale, _lib.BF16)
+    desc = _lib.make_desc(B, H, N, D, n_pos, has_cls, _lib.BF16, _lib.BF16, scale)
+    ref = [torch.empty_like(q) for _ in range(3)]
+    delta = torch.empty(B, H, N, device=DEV, dtype=torch.float32)
+    _lib.attn_bwd(desc, q, k, v, o, do, lse, rope, *ref, delta)
+    got = [torch.full_like(q, float("nan")) for _ in range(3)]
+    _lib.attn_bwd_noalloc(desc, q, k, v, o, do, lse, rope, *got)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("dQ", "dK", "dV"), got, ref):
+        assert torch.isfinite(a).all(), name
+        assert torch.equal(a, b), f"{name}: max diff {(a.float() - b.float()).abs().max().item():.3e}"
+    return _lib.tile_config(desc, 1)[0]
+
+
+def test_noalloc_matches_workspace_entry_two_calls():
+    assert _one(4, 6, 16, True, 64, seed=21) == 1    # split path, N = 257
+    assert _one(2, 3, 7, True, 128, seed=22) == 1    # smaller, split path (D = 128)
+    assert _one(2, 4, 14, True, 64, seed=23) == 0    # one-pass path (no workspace used)

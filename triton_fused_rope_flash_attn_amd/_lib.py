@@ -20,7 +20,9 @@ DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
 # Status codes (farope_status).
 OK = 0
-ERR_NULL, ERR_HEAD_DIM, ERR_SEQ_LEN, ERR_DTYPE, ERR_TABLE, ERR_SHAPE, ERR_LAUNCH, ERR_ALIGN = range(1, 9)
+(ERR_NULL, ERR_HEAD_DIM, ERR_SEQ_LEN, ERR_DTYPE, ERR_TABLE, ERR_SHAPE, ERR_LAUNCH, ERR_ALIGN,
+ ERR_SCRATCH) = range(1, 10)
+NOALLOC_MAX_ROWS = 4194304   # FAROPE_NOALLOC_MAX_ROWS
 
 # Every function the header declares; tests check the library exports all of them.
 EXPORTS = (
@@ -33,6 +35,7 @@ EXPORTS = (
     "farope_attn_bwd_dk_dv",
     "farope_attn_bwd_dq",
     "farope_attn_bwd",
+    "farope_attn_bwd_noalloc",
     "farope_tile_config",
 )
 
@@ -73,6 +76,10 @@ _SIGNATURES = {
     "farope_attn_bwd": (
         ctypes.c_int,
         [_D, _P, _S, _P, _S, _P, _S, _P, _S, _P, _S, _P, _P, _P, _S, _P, _S, _P, _S, _P, _P],
+    ),
+    "farope_attn_bwd_noalloc": (
+        ctypes.c_int,
+        [_D, _P, _S, _P, _S, _P, _S, _P, _S, _P, _S, _P, _P, _P, _S, _P, _S, _P, _S, _P],
     ),
     "farope_tile_config": (ctypes.c_int, [_D, _I32, ctypes.POINTER(ctypes.c_int32)]),
 }
@@ -159,6 +166,19 @@ def attn_bwd(desc: AttnDesc, q, k, v, o, do, lse, rope, dq, dk, dv, delta) -> No
         delta.data_ptr(), stream_of(q),
     )
     check(rc, "farope_attn_bwd")
+
+
+def attn_bwd_noalloc(desc: AttnDesc, q, k, v, o, do, lse, rope, dq, dk, dv) -> None:
+    """farope_attn_bwd_noalloc: the backward with the library's static delta workspace."""
+    rc = load().farope_attn_bwd_noalloc(
+        ctypes.byref(desc),
+        q.data_ptr(), strides(q), k.data_ptr(), strides(k), v.data_ptr(), strides(v),
+        o.data_ptr(), strides(o), do.data_ptr(), strides(do),
+        lse.data_ptr(), rope.data_ptr(),
+        dq.data_ptr(), strides(dq), dk.data_ptr(), strides(dk), dv.data_ptr(), strides(dv),
+        stream_of(q),
+    )
+    check(rc, "farope_attn_bwd_noalloc")
 
 
 def attn_bwd_preprocess(desc: AttnDesc, o, do, delta) -> None:

@@ -11,6 +11,13 @@
 
 using namespace farope;
 
+// Workspace of farope_attn_bwd_noalloc: the split backward's delta rows (fp32,
+// one per query row of the call, B*H*N <= FAROPE_NOALLOC_MAX_ROWS = 16 MiB).
+// The runtime gives every device its own copy when it loads the code object,
+// held until the process ends.  In host code this name is only a handle for
+// hipGetSymbolAddress: kernels receive the device address it returns.
+static __device__ __align__(256) float scratch[FAROPE_NOALLOC_MAX_ROWS];
+
 namespace farope {
 
 // Resident-capacity query for persistent kernels, cached per (device, kernel).
@@ -121,6 +128,83 @@ int fill_common(BwdParams& p, const farope_attn_desc* d, const float* rope) {
 
 int launch_rc(hipError_t e) { return e == hipSuccess ? FAROPE_OK : FAROPE_ERR_LAUNCH; }
 
+// Device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.
+constexpr int kMaxDevices = 64;
+constexpr int64_t kScratchFloats = FAROPE_NOALLOC_MAX_ROWS;
+
+int scratch_ptr(float** out) {
+  static std::mutex mu;
+  static float* ptrs[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return FAROPE_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return FAROPE_ERR_LAUNCH;
+    ptrs[dev] = static_cast<float*>(ptr);
+  }
+  *out = ptrs[dev];
+  return FAROPE_OK;
+}
+
+int bwd_impl(const farope_attn_desc* desc, const void* q, const int64_t q_stride[4],
+             const void* k, const int64_t k_stride[4], const void* v, const int64_t v_stride[4],
+             const void* o, const int64_t o_stride[4], const void* dout,
+             const int64_t dout_stride[4], const float* lse, const float* rope_packed, void* dq,
+             const int64_t dq_stride[4], void* dk, const int64_t dk_stride[4], void* dv,
+             const int64_t dv_stride[4], float* delta_ws, bool static_ws, void* stream) {
+  FAROPE_TRY(check_desc(desc));
+  if (!q_stride || !k_stride || !v_stride || !o_stride || !dout_stride || !dq_stride ||
+      !dk_stride || !dv_stride)
+    return FAROPE_ERR_NULL;
+  const int es = elem_size(desc->io_dtype);
+  FAROPE_TRY(check_ptr(q, es));
+  FAROPE_TRY(check_ptr(k, es));
+  FAROPE_TRY(check_ptr(v, es));
+  FAROPE_TRY(check_ptr(o, es));
+  FAROPE_TRY(check_ptr(dout, es));
+  FAROPE_TRY(check_ptr(dq, es));
+  FAROPE_TRY(check_ptr(dk, es));
+  FAROPE_TRY(check_ptr(dv, es));
+  FAROPE_TRY(check_ptr(lse, 4));
+  FAROPE_TRY(check_ptr(rope_packed, 16));
+  const bool fused = bwd_fused(desc);
+  if (static_ws) {
+    // the split path's delta rows go to this device's static scratch array
+    if ((int64_t)desc->batch * desc->heads * desc->seq_len > kScratchFloats) return FAROPE_ERR_SCRATCH;
+    FAROPE_TRY(scratch_ptr(&delta_ws));
+  } else if (!fused) {
+    FAROPE_TRY(check_ptr(delta_ws, 4));
+  }
+  BwdParams p = {};
+  fill_common(p, desc, rope_packed);
+  p.q = q; p.k = k; p.v = v; p.o = o; p.dout = dout;
+  p.dq = dq; p.dk = dk; p.dv = dv;
+  p.lse = lse; p.delta = delta_ws;
+  copy4(p.sq, q_stride); copy4(p.sk, k_stride); copy4(p.sv, v_stride); copy4(p.so, o_stride);
+  copy4(p.sdo, dout_stride); copy4(p.sdq, dq_stride); copy4(p.sdk, dk_stride);
+  copy4(p.sdv, dv_stride);
+  p.vec_q = vec_ok(q, q_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_k = vec_ok(k, k_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_v = vec_ok(v, v_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_o = vec_ok(o, o_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_do = vec_ok(dout, dout_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_dq = vec_out_ok(dq, dq_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_dk = vec_out_ok(dk, dk_stride, es, desc->seq_len, desc->head_dim);
+  p.vec_dv = vec_out_ok(dv, dv_stride, es, desc->seq_len, desc->head_dim);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const int D = desc->head_dim;
+  if (fused) {
+    p.n_blk = 1;
+    return launch_rc(launch_bwd_fused(p, desc->io_dtype, desc->compute_dtype, st));
+  }
+  p.n_blk = cdiv(p.N, bwd_dq_block_rows(D, desc->compute_dtype));
+  FAROPE_TRY(launch_rc(launch_bwd_dq(p, desc->io_dtype, desc->compute_dtype, D, true, st)));
+  p.n_blk = cdiv(p.N, bwd_dkdv_block_rows(D, desc->compute_dtype));
+  return launch_rc(launch_bwd_dkdv(p, desc->io_dtype, desc->compute_dtype, D, st));
+}
+
 }  // namespace
 
 extern "C" {
@@ -139,6 +223,9 @@ const char* farope_strerror(int status) {
     case FAROPE_ERR_SHAPE: return "farope: batch/heads must be positive and B*H <= 2^30";
     case FAROPE_ERR_LAUNCH: return "farope: HIP kernel launch failed";
     case FAROPE_ERR_ALIGN: return "farope: pointer not aligned to its element size";
+    case FAROPE_ERR_SCRATCH:
+      return "farope: batch*heads*seq_len exceeds the static workspace of farope_attn_bwd_noalloc "
+             "(FAROPE_NOALLOC_MAX_ROWS = 4194304); use farope_attn_bwd with a caller workspace";
     default: return "farope: unknown status";
   }
 }
@@ -303,49 +390,20 @@ int farope_attn_bwd(const farope_attn_desc* desc, const void* q, const int64_t q
                     const float* rope_packed, void* dq, const int64_t dq_stride[4], void* dk,
                     const int64_t dk_stride[4], void* dv, const int64_t dv_stride[4],
                     float* delta_ws, void* stream) {
-  FAROPE_TRY(check_desc(desc));
-  if (!q_stride || !k_stride || !v_stride || !o_stride || !dout_stride || !dq_stride ||
-      !dk_stride || !dv_stride)
-    return FAROPE_ERR_NULL;
-  const int es = elem_size(desc->io_dtype);
-  FAROPE_TRY(check_ptr(q, es));
-  FAROPE_TRY(check_ptr(k, es));
-  FAROPE_TRY(check_ptr(v, es));
-  FAROPE_TRY(check_ptr(o, es));
-  FAROPE_TRY(check_ptr(dout, es));
-  FAROPE_TRY(check_ptr(dq, es));
-  FAROPE_TRY(check_ptr(dk, es));
-  FAROPE_TRY(check_ptr(dv, es));
-  FAROPE_TRY(check_ptr(lse, 4));
-  FAROPE_TRY(check_ptr(rope_packed, 16));
-  const bool fused = bwd_fused(desc);
-  if (!fused) FAROPE_TRY(check_ptr(delta_ws, 4));
-  BwdParams p = {};
-  fill_common(p, desc, rope_packed);
-  p.q = q; p.k = k; p.v = v; p.o = o; p.dout = dout;
-  p.dq = dq; p.dk = dk; p.dv = dv;
-  p.lse = lse; p.delta = delta_ws;
-  copy4(p.sq, q_stride); copy4(p.sk, k_stride); copy4(p.sv, v_stride); copy4(p.so, o_stride);
-  copy4(p.sdo, dout_stride); copy4(p.sdq, dq_stride); copy4(p.sdk, dk_stride);
-  copy4(p.sdv, dv_stride);
-  p.vec_q = vec_ok(q, q_stride, es, desc->seq_len, desc->head_dim);
-  p.vec_k = vec_ok(k, k_stride, es, desc->seq_len, desc->head_dim);
-  p.vec_v = vec_ok(v, v_stride, es, desc->seq_len, desc->head_dim);
-  p.vec_o = vec_ok(o, o_stride, es, desc->seq_len, desc->head_dim);
-  p.vec_do = vec_ok(dout, dout_stride, es, desc->seq_len, desc->head_dim);
-  p.vec_dq = vec_out_ok(dq, dq_stride, es, desc->seq_len, desc->head_dim);
-  p.vec_dk = vec_out_ok(dk, dk_stride, es, desc->seq_len, desc->head_dim);
-  p.vec_dv = vec_out_ok(dv, dv_stride, es, desc->seq_len, desc->head_dim);
-  const hipStream_t st = static_cast<hipStream_t>(stream);
-  const int D = desc->head_dim;
-  if (fused) {
-    p.n_blk = 1;
-    return launch_rc(launch_bwd_fused(p, desc->io_dtype, desc->compute_dtype, st));
-  }
-  p.n_blk = cdiv(p.N, bwd_dq_block_rows(D, desc->compute_dtype));
-  FAROPE_TRY(launch_rc(launch_bwd_dq(p, desc->io_dtype, desc->compute_dtype, D, true, st)));
-  p.n_blk = cdiv(p.N, bwd_dkdv_block_rows(D, desc->compute_dtype));
-  return launch_rc(launch_bwd_dkdv(p, desc->io_dtype, desc->compute_dtype, D, st));
+  return bwd_impl(desc, q, q_stride, k, k_stride, v, v_stride, o, o_stride, dout, dout_stride, lse,
+                  rope_packed, dq, dq_stride, dk, dk_stride, dv, dv_stride, delta_ws, false, stream);
+}
+
+int farope_attn_bwd_noalloc(const farope_attn_desc* desc, const void* q,
+                            const int64_t q_stride[4], const void* k, const int64_t k_stride[4],
+                            const void* v, const int64_t v_stride[4], const void* o,
+                            const int64_t o_stride[4], const void* dout,
+                            const int64_t dout_stride[4], const float* lse,
+                            const float* rope_packed, void* dq, const int64_t dq_stride[4],
+                            void* dk, const int64_t dk_stride[4], void* dv,
+                            const int64_t dv_stride[4], void* stream) {
+  return bwd_impl(desc, q, q_stride, k, k_stride, v, v_stride, o, o_stride, dout, dout_stride, lse,
+                  rope_packed, dq, dq_stride, dk, dk_stride, dv, dv_stride, nullptr, true, stream);
 }
 
 }  // extern "C"
