@@ -12,7 +12,9 @@ Prints one JSON line (the driver's contract) carrying:
                  stream, vs 8 TB/s; `traffic` = measured HBM bytes per launch
                  from the committed rocprofv3 counter summary, if present
   cpu_baseline   the PyTorch oracle (Python RoPE + torch SDPA, fp32) on the
-                 host CPU over a bounded slice of the same workload
+                 host CPU at BASELINE.json configs[0] (B=2 H=8 N=197 D=64,
+                 loss o.sum()); `workload_slice` adds the same oracle on a
+                 bounded slice of the bench workload
   torch_rocm     the same oracle on the GPU in bf16 (torch-ROCm SDPA + RoPE)
 
 The GPU leaves its idle clocks only after some tens of milliseconds of
@@ -96,8 +98,81 @@ def make_inputs(wl, device, seed=0, dtype=None):
     return [t.to(dtype).to(device) for t in ts]
 
 
-def time_cpu_baseline(wl, budget_s=12.0):
-    """Oracle fwd+bwd in fp32 on the host over a slice of the workload's batch.
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for ln in fh:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def _cpu_threads() -> int:
+    cores = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        cores = min(cores, int(os.environ["OMP_NUM_THREADS"]))
+    return cores
+
+
+def time_cpu_config0(budget_s=8.0):
+    """BASELINE.json configs[0], the reference's CPU-runnable case: Python 2D
+    RoPE + torch SDPA (math), fp32, B=2, H=8, H_img=14 + CLS (N=197), D=64,
+    q/k/v ~ N(0,1) drawn in that order from seed 0, CosSinTable base 100,
+    loss = o.sum() so dO = ones.  Forward and backward are timed separately
+    (time.perf_counter), 3 warm-ups, then the median over at least 10 runs
+    and about `budget_s` seconds."""
+    import torch
+    from oracle import torch_ref
+    from triton_fused_rope_flash_attn_amd import build_axial_rope_pairs
+
+    cores = _cpu_threads()
+    torch.set_num_threads(cores)
+    B, H, side, D = 2, 8, 14, 64
+    N = side * side + 1
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(B, H, N, D, generator=g) for _ in range(3))
+    cosp, sinp = build_axial_rope_pairs(side, D, torch.device("cpu"), base=100.0)
+
+    def once():
+        qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+        t0 = time.perf_counter()
+        o = torch_ref.attention(qq, kk, vv, cosp, sinp, True)
+        t1 = time.perf_counter()
+        o.sum().backward()
+        t2 = time.perf_counter()
+        return t1 - t0, t2 - t1
+
+    for _ in range(3):
+        once()
+    tf, tb = [], []
+    t_start = time.perf_counter()
+    while len(tf) < 10 or time.perf_counter() - t_start < budget_s:
+        a, b = once()
+        tf.append(a)
+        tb.append(b)
+    mf, mb = statistics.median(tf), statistics.median(tb)
+    f_fwd, f_bwd, _ = flops(B, H, N, D)
+    return {
+        "value": (f_fwd + f_bwd) / (mf + mb) / 1e12,
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (
+            f"BASELINE configs[0]: oracle (Python 2D RoPE + torch SDPA math, fp32, autograd), B={B} H={H} "
+            f"N={N} D={D}, q/k/v ~ N(0,1) seed 0, base 100, loss o.sum() (dO = ones); median of {len(tf)} "
+            f"runs ({time.perf_counter() - t_start:.1f} s): fwd {mf * 1e3:.2f} ms, bwd {mb * 1e3:.2f} ms; "
+            f"{cores} threads; CPU: {_cpu_model()}"
+        ),
+        "fwd_ms": round(mf * 1e3, 3),
+        "bwd_ms": round(mb * 1e3, 3),
+    }
+
+
+def time_cpu_baseline(wl, budget_s=6.0):
+    """Oracle fwd+bwd in fp32 on the host over a slice of the bench workload's
+    batch (the like-for-like TFLOP/s at the GPU's shape and dO ~ N(0,1)).
 
     Runs whole fwd+bwd iterations until `budget_s` seconds of CPU work have
     been timed (at least 3), with the thread count capped at the process's
@@ -106,9 +181,7 @@ def time_cpu_baseline(wl, budget_s=12.0):
     from oracle import torch_ref
     from triton_fused_rope_flash_attn_amd import build_axial_rope_pairs
 
-    cores = len(os.sched_getaffinity(0))
-    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
-        cores = min(cores, int(os.environ["OMP_NUM_THREADS"]))
+    cores = _cpu_threads()
     torch.set_num_threads(cores)
     sub = dict(wl, B=4 if wl["D"] == 64 else 1)
     q, k, v, do = make_inputs(sub, "cpu", dtype=torch.float32)
@@ -123,15 +196,6 @@ def time_cpu_baseline(wl, budget_s=12.0):
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
     _, _, fall = flops(B, H, N, D)
-    cpu_model = ""
-    try:
-        with open("/proc/cpuinfo") as fh:
-            for ln in fh:
-                if ln.startswith("model name"):
-                    cpu_model = ln.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
     return {
         "value": fall / med / 1e12,
         "unit": "TFLOP/s",
@@ -139,8 +203,9 @@ def time_cpu_baseline(wl, budget_s=12.0):
         "kind": "port",
         "sample": (
             f"oracle (Python 2D RoPE + torch SDPA math, fp32, autograd) fwd+bwd on B={B} of "
-            f"{wl['B']} (planes {B * H} of {wl['B'] * H}), N={N}, D={D}; median of {len(times)} "
-            f"iterations ({sum(times):.1f} s timed), {med * 1e3:.1f} ms each; {cores} threads; CPU: {cpu_model}"
+            f"{wl['B']} (planes {B * H} of {wl['B'] * H}), N={N}, D={D}, dO ~ N(0,1); median of "
+            f"{len(times)} iterations ({sum(times):.1f} s timed), {med * 1e3:.1f} ms each; {cores} "
+            f"threads; CPU: {_cpu_model()}"
         ),
     }
 
@@ -431,7 +496,8 @@ def main():
         if args.compile:
             result["vit_block_compiled"] = time_block(wl, max(10, args.steps // 4), 3, compiled=True)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = time_cpu_baseline(wl)
+        result["cpu_baseline"] = time_cpu_config0()
+        result["cpu_baseline"]["workload_slice"] = time_cpu_baseline(wl)
     print(json.dumps(result), flush=True)
 
 
