@@ -35,7 +35,7 @@ typedef enum farope_dtype {
 typedef enum farope_status {
   FAROPE_OK = 0,
   FAROPE_ERR_NULL = 1,        /* a required pointer is NULL */
-  FAROPE_ERR_HEAD_DIM = 2,    /* head_dim not supported (needs D % 4 == 0; kernels: 32, 64, 128) */
+  FAROPE_ERR_HEAD_DIM = 2,    /* head_dim not supported (needs D % 4 == 0; kernels: 32, 64, 128, 256) */
   FAROPE_ERR_SEQ_LEN = 3,     /* seq_len != n_pos + has_cls, or seq_len < 1 */
   FAROPE_ERR_DTYPE = 4,       /* unknown io or compute dtype */
   FAROPE_ERR_TABLE = 5,       /* RoPE table geometry inconsistent with the call */

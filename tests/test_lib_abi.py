@@ -65,7 +65,8 @@ def test_rope_packed_elems(lib):
 
 @pytest.mark.parametrize(
     "N,D,has_cls,fwd_items,bwd_var",
-    [(197, 64, 1, 1, 0), (256, 64, 0, 1, 0), (257, 64, 1, 2, 1), (1025, 128, 1, 9, 1), (197, 128, 1, 2, 1)],
+    [(197, 64, 1, 1, 0), (256, 64, 0, 1, 0), (257, 64, 1, 2, 1), (1025, 128, 1, 9, 1), (197, 128, 1, 2, 1),
+     (197, 256, 1, 4, 1), (257, 256, 1, 5, 1)],
 )
 def test_tile_table(lib, N, D, has_cls, fwd_items, bwd_var):
     desc = _lib.make_desc(8, 12, N, D, N - has_cls, has_cls, _lib.BF16, _lib.BF16, D ** -0.5)
@@ -95,6 +96,7 @@ def _call_fwd(lib, desc, q=16, lse=16, rope=16):
     [
         (dict(D=66), _lib.ERR_HEAD_DIM),
         (dict(D=96), _lib.ERR_HEAD_DIM),
+        (dict(D=512), _lib.ERR_HEAD_DIM),
         (dict(N=198), _lib.ERR_SEQ_LEN),
         (dict(io=7), _lib.ERR_DTYPE),
         (dict(ct=9), _lib.ERR_DTYPE),

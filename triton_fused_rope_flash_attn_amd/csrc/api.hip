@@ -62,7 +62,8 @@ int check_desc(const farope_attn_desc* d) {
   if (d->batch <= 0 || d->heads <= 0) return FAROPE_ERR_SHAPE;
   if ((int64_t)d->batch * d->heads > (int64_t)(1 << 30)) return FAROPE_ERR_SHAPE;
   if (d->head_dim <= 0 || d->head_dim % 4 != 0) return FAROPE_ERR_HEAD_DIM;
-  if (d->head_dim != 32 && d->head_dim != 64 && d->head_dim != 128) return FAROPE_ERR_HEAD_DIM;
+  if (d->head_dim != 32 && d->head_dim != 64 && d->head_dim != 128 && d->head_dim != 256)
+    return FAROPE_ERR_HEAD_DIM;
   if (d->has_cls != 0 && d->has_cls != 1) return FAROPE_ERR_SEQ_LEN;
   if (d->n_pos < 1 || d->seq_len != d->n_pos + d->has_cls) return FAROPE_ERR_SEQ_LEN;
   if (!dtype_ok(d->io_dtype) || !dtype_ok(d->compute_dtype)) return FAROPE_ERR_DTYPE;
@@ -216,7 +217,7 @@ const char* farope_strerror(int status) {
     case FAROPE_OK: return "success";
     case FAROPE_ERR_NULL: return "farope: a required pointer is NULL";
     case FAROPE_ERR_HEAD_DIM:
-      return "farope: unsupported head_dim (must be divisible by 4; kernels exist for 32, 64 and 128)";
+      return "farope: unsupported head_dim (must be divisible by 4; kernels exist for 32, 64, 128 and 256)";
     case FAROPE_ERR_SEQ_LEN: return "farope: seq_len must equal n_pos + has_cls";
     case FAROPE_ERR_DTYPE: return "farope: unsupported dtype (float32, float16, bfloat16)";
     case FAROPE_ERR_TABLE: return "farope: RoPE table geometry does not match the call";

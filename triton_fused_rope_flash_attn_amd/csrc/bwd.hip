@@ -638,26 +638,47 @@ template <> struct BwdShape<128, true> {
   static constexpr int DQ_NW = 8, DQ_QT = 1, DQ_KVS = 64;
   static constexpr int KV_NW = 8, KV_KT = 1, KV_QS = 64;
 };
+// D = 256: one wave per SIMD (4-wave workgroups), so each wave may hold up to
+// 512 registers (VGPRs plus AGPRs): the dK / dV accumulators alone are 128
+// per wave.  32-row stages keep the prefetch registers and the fp32 tiles
+// (with their transposed copies) within registers and LDS.
+template <> struct BwdShape<256, false> {
+  static constexpr int DQ_NW = 4, DQ_QT = 1, DQ_KVS = 32;
+  static constexpr int KV_NW = 4, KV_KT = 1, KV_QS = 32;
+};
+template <> struct BwdShape<256, true> {
+  static constexpr int DQ_NW = 4, DQ_QT = 1, DQ_KVS = 32;
+  static constexpr int KV_NW = 4, KV_KT = 1, KV_QS = 32;
+};
 
 template <int D, bool F32C> static int dq_rows() { return BwdShape<D, F32C>::DQ_NW * BwdShape<D, F32C>::DQ_QT * 16; }
 template <int D, bool F32C> static int kv_rows() { return BwdShape<D, F32C>::KV_NW * BwdShape<D, F32C>::KV_KT * 16; }
 int bwd_dq_block_rows(int D, int ct) {
   const bool f = ct == DT_F32;
-  if (D == 32) return f ? dq_rows<32, true>() : dq_rows<32, false>();
-  return D == 64 ? (f ? dq_rows<64, true>() : dq_rows<64, false>())
-                 : (f ? dq_rows<128, true>() : dq_rows<128, false>());
+  switch (D) {
+    case 32: return f ? dq_rows<32, true>() : dq_rows<32, false>();
+    case 64: return f ? dq_rows<64, true>() : dq_rows<64, false>();
+    case 128: return f ? dq_rows<128, true>() : dq_rows<128, false>();
+    default: return f ? dq_rows<256, true>() : dq_rows<256, false>();
+  }
 }
 int bwd_dkdv_block_rows(int D, int ct) {
   const bool f = ct == DT_F32;
-  if (D == 32) return f ? kv_rows<32, true>() : kv_rows<32, false>();
-  return D == 64 ? (f ? kv_rows<64, true>() : kv_rows<64, false>())
-                 : (f ? kv_rows<128, true>() : kv_rows<128, false>());
+  switch (D) {
+    case 32: return f ? kv_rows<32, true>() : kv_rows<32, false>();
+    case 64: return f ? kv_rows<64, true>() : kv_rows<64, false>();
+    case 128: return f ? kv_rows<128, true>() : kv_rows<128, false>();
+    default: return f ? kv_rows<256, true>() : kv_rows<256, false>();
+  }
 }
 int bwd_dkdv_threads(int D, int ct) {
   const bool f = ct == DT_F32;
-  if (D == 32) return 64 * (f ? BwdShape<32, true>::KV_NW : BwdShape<32, false>::KV_NW);
-  return 64 * (D == 64 ? (f ? BwdShape<64, true>::KV_NW : BwdShape<64, false>::KV_NW)
-                       : (f ? BwdShape<128, true>::KV_NW : BwdShape<128, false>::KV_NW));
+  switch (D) {
+    case 32: return 64 * (f ? BwdShape<32, true>::KV_NW : BwdShape<32, false>::KV_NW);
+    case 64: return 64 * (f ? BwdShape<64, true>::KV_NW : BwdShape<64, false>::KV_NW);
+    case 128: return 64 * (f ? BwdShape<128, true>::KV_NW : BwdShape<128, false>::KV_NW);
+    default: return 64 * (f ? BwdShape<256, true>::KV_NW : BwdShape<256, false>::KV_NW);
+  }
 }
 
 template <typename IO, int D>
@@ -684,10 +705,17 @@ hipError_t launch_bwd_pre(const BwdParams& p, int io, int D, hipStream_t st) {
       default: return pre_io<float, 64>(p, st);
     }
   }
+  if (D == 128) {
+    switch (io) {
+      case DT_BF16: return pre_io<bf16, 128>(p, st);
+      case DT_F16: return pre_io<f16, 128>(p, st);
+      default: return pre_io<float, 128>(p, st);
+    }
+  }
   switch (io) {
-    case DT_BF16: return pre_io<bf16, 128>(p, st);
-    case DT_F16: return pre_io<f16, 128>(p, st);
-    default: return pre_io<float, 128>(p, st);
+    case DT_BF16: return pre_io<bf16, 256>(p, st);
+    case DT_F16: return pre_io<f16, 256>(p, st);
+    default: return pre_io<float, 256>(p, st);
   }
 }
 
@@ -756,7 +784,8 @@ hipError_t launch_bwd_dq(const BwdParams& p, int io, int ct, int D, bool write_d
   switch (D) {
     case 32: return dq_io<32>(p, io, ct, write_delta, st);
     case 64: return dq_io<64>(p, io, ct, write_delta, st);
-    default: return dq_io<128>(p, io, ct, write_delta, st);
+    case 128: return dq_io<128>(p, io, ct, write_delta, st);
+    default: return dq_io<256>(p, io, ct, write_delta, st);
   }
 }
 
@@ -780,7 +809,8 @@ hipError_t launch_bwd_dkdv(const BwdParams& p, int io, int ct, int D, hipStream_
   switch (D) {
     case 32: return kv_io<32>(p, io, ct, st);
     case 64: return kv_io<64>(p, io, ct, st);
-    default: return kv_io<128>(p, io, ct, st);
+    case 128: return kv_io<128>(p, io, ct, st);
+    default: return kv_io<256>(p, io, ct, st);
   }
 }
 

@@ -103,10 +103,13 @@ fwd_kernel(const FwdParams p) {
 
   // 16-bit compute: V is kept row-major (raw rows when IO is the compute
   // type) and V^T fragments are read transposed (ds_read_b64_tr_b16); fp32
-  // compute keeps an explicitly transposed V^T tile.
+  // compute keeps an explicitly transposed V^T tile, except at D = 256, where
+  // two transposed fp32 tiles do not fit next to the K-hat ring: V stays
+  // row-major and each V^T fragment is gathered element by element (VROW).
   constexpr bool TRV = sizeof(S) == 2;
+  constexpr bool VROW = !TRV && D >= 256;
   __shared__ __attribute__((aligned(16))) S sK[2][KC * LDK];
-  __shared__ __attribute__((aligned(16))) S sVt[2][TRV ? KC * LDK : D * LDV];
+  __shared__ __attribute__((aligned(16))) S sVt[2][(TRV || VROW) ? KC * LDK : D * LDV];
   // LDS copy of the packed table: D/2 (cos, sin) pairs = D floats per row,
   // 16-byte chunk c of row r stored at chunk c ^ (r & (D/4 - 1)) (bank-spread
   // without padding).
@@ -271,7 +274,7 @@ fwd_kernel(const FwdParams p) {
             rope_rotate8(xk, pcs[it][x]);
           }
           C::put8(&sK[slot][kperm(2 * rp + x) * LDK + 8 * cc], xk);
-          if constexpr (TRV) {
+          if constexpr (TRV || VROW) {
             S* dst = &sVt[slot][(2 * rp + x) * LDK + 8 * cc];
             if constexpr (std::is_same<IO, S>::value) {
               *reinterpret_cast<typename Raw8<IO>::vec*>(dst) = pv[it][x].v;   // raw row segment
@@ -284,7 +287,7 @@ fwd_kernel(const FwdParams p) {
             unpack8(pv[it][x], xv[x]);
           }
         }
-        if constexpr (!TRV) {
+        if constexpr (!TRV && !VROW) {
 #pragma unroll
           for (int e = 0; e < 8; ++e)
             put2<CT>(&sVt[slot][(8 * cc + e) * LDV + vswz(8 * cc + e, 2 * rp)], xv[0][e], xv[1][e]);
@@ -361,6 +364,14 @@ fwd_kernel(const FwdParams p) {
   // workgroup then runs the same instruction stream with no per-subtile
   // guards, and for the 16-row-ragged N of ViT planes the extra work lands on
   // SIMDs that would otherwise wait at the next barrier.
+  // VROW: V^T fragment (rows 16d.., k-slot e <-> key 32j + 8lg + e) gathered
+  // from the row-major V tile, one element per key row.
+  auto vrow_frag = [&](const S* __restrict__ cV, int j, int d) __attribute__((always_inline)) {
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = (float)cV[(32 * j + 8 * lg + e) * LDK + 16 * d + lr];
+    return C::make(x);
+  };
   using SAcc = f32x4[QT][2];
   using KFr = Frag[KS][2];
   using VFr = Frag[DT];
@@ -378,6 +389,8 @@ fwd_kernel(const FwdParams p) {
       if constexpr (TRV)
         vf[d] = C::tr(cV + tr_offset(32 * j + 8 * lg, 16 * d, LDK, lr),
                       cV + tr_offset(32 * j + 8 * lg + 4, 16 * d, LDK, lr));
+      else if constexpr (VROW)
+        vf[d] = vrow_frag(cV, j, d);
       else
         vf[d] = C::lds(&cV[(16 * d + lr) * LDV + vswz(16 * d + lr, 32 * j + 8 * lg)]);
     }
@@ -596,6 +609,8 @@ fwd_kernel(const FwdParams p) {
       Frag a;
       if constexpr (TRV)
         a = C::tr(cV + tr_offset(32 * j + 8 * lg, 16 * d, LDK, lr), cV + tr_offset(32 * j + 8 * lg + 4, 16 * d, LDK, lr));
+      else if constexpr (VROW)
+        a = vrow_frag(cV, j, d);
       else
         a = C::lds(&cV[(16 * d + lr) * LDV + vswz(16 * d + lr, 32 * j + 8 * lg)]);
 #pragma unroll
@@ -808,13 +823,19 @@ template <int D> struct FwdShape;
 template <> struct FwdShape<32> { static constexpr int NW = 8, QT = 2, KC = 128, TABROWS = 257; };
 template <> struct FwdShape<64> { static constexpr int NW = 8, QT = 2, KC = 128, TABROWS = 257; };
 template <> struct FwdShape<128> { static constexpr int NW = 8, QT = 1, KC = 64, TABROWS = 0; };
+// D = 256: one wave per SIMD (4-wave workgroups), so each wave may hold up to
+// 512 registers (VGPRs plus AGPRs): the O accumulators alone are 64 per wave.
+template <> struct FwdShape<256> { static constexpr int NW = 4, QT = 1, KC = 32, TABROWS = 0; };
 
 template <int D> static int fwd_rows() { return FwdShape<D>::NW * FwdShape<D>::QT * 16; }
 int fwd_block_rows(int D) {
-  return D == 32 ? fwd_rows<32>() : D == 64 ? fwd_rows<64>() : fwd_rows<128>();
+  return D == 32 ? fwd_rows<32>() : D == 64 ? fwd_rows<64>() : D == 128 ? fwd_rows<128>() : fwd_rows<256>();
 }
 int fwd_threads(int D) {
-  return 64 * (D == 32 ? FwdShape<32>::NW : D == 64 ? FwdShape<64>::NW : FwdShape<128>::NW);
+  return 64 * (D == 32    ? FwdShape<32>::NW
+               : D == 64  ? FwdShape<64>::NW
+               : D == 128 ? FwdShape<128>::NW
+                          : FwdShape<256>::NW);
 }
 
 template <typename IO, int CT, int D>
@@ -841,7 +862,8 @@ static hipError_t fwd_shape(const FwdParams& p, int D, hipStream_t st) {
   switch (D) {
     case 32: return fwd_launch<IO, CT, 32>(p, st);
     case 64: return fwd_launch<IO, CT, 64>(p, st);
-    default: return fwd_launch<IO, CT, 128>(p, st);
+    case 128: return fwd_launch<IO, CT, 128>(p, st);
+    default: return fwd_launch<IO, CT, 256>(p, st);
   }
 }
 
