@@ -66,7 +66,10 @@ __global__ void __launch_bounds__(256) bwd_pre_kernel(const BwdParams p) {
 // into registers while the current block is computed (buffer descriptors over
 // the plane, rows >= N read 0); their table rows are read when the block is
 // committed.  Otherwise each block is loaded synchronously.
-template <typename IO, int CT, int D, int NW, int QT, int KVS, bool WRITE_DELTA, bool VEC>
+// PS (bf16 compute, head_dim >= 128): logits from split K-hat (LDS, hi + lo)
+// and Q-hat (registers, hi + lo) as in the forward pass, and dQ-hat from
+// dS = hi + lo: dQ-hat^T += K-hat^T dS_hi^T + K-hat^T dS_lo^T.
+template <typename IO, int CT, int D, int NW, int QT, int KVS, bool WRITE_DELTA, bool VEC, bool PS>
 __global__ void __launch_bounds__(NW * 64)
 bwd_dq_kernel(const BwdParams p) {
   using C = Comp<CT>;
@@ -82,7 +85,9 @@ bwd_dq_kernel(const BwdParams p) {
   // fp32 storage keeps an explicit transposed copy.
   constexpr bool TR = sizeof(S) == 2;
 
+  static_assert(!PS || CT == DT_BF16, "split operands are bf16");
   __shared__ __attribute__((aligned(16))) S sK[KVS * LDK];
+  __shared__ __attribute__((aligned(16))) S sKl[PS ? KVS * LDK : 8];   // PS: K-hat lo
   __shared__ __attribute__((aligned(16))) S sKt[TR ? 8 : D * LDT];
   __shared__ __attribute__((aligned(16))) S sV[KVS * LDK];
 
@@ -106,6 +111,7 @@ bwd_dq_kernel(const BwdParams p) {
   const int lr = lane & 15, lg = lane >> 4;
 
   Frag qf[QT][KS], gf[QT][KS];
+  Frag qfl[PS ? QT : 1][PS ? KS : 1];   // PS: Q-hat lo
   float lse2[QT], dlt[QT];
   int qrow[QT];
 #pragma unroll
@@ -133,7 +139,10 @@ bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = g[e] = 0.f;
       }
-      qf[t][s] = C::make(x);
+      if constexpr (PS)
+        split_bf16x8(x, qf[t][s].v, qfl[t][s].v);
+      else
+        qf[t][s] = C::make(x);
       gf[t][s] = C::make(g);
     }
     if (WRITE_DELTA) {
@@ -152,6 +161,18 @@ bwd_dq_kernel(const BwdParams p) {
   for (int t = 0; t < QT; ++t)
 #pragma unroll
     for (int d = 0; d < DT; ++d) dqacc[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // K-hat row segment -> sK (PS: hi to sK, lo to sKl)
+  auto put_khat = [&](int off, const float (&xk)[8]) __attribute__((always_inline)) {
+    if constexpr (PS) {
+      bf16x8 hi, lo;
+      split_bf16x8(xk, hi, lo);
+      *reinterpret_cast<bf16x8*>(&sK[off]) = hi;
+      *reinterpret_cast<bf16x8*>(&sKl[off]) = lo;
+    } else {
+      C::put8(&sK[off], xk);
+    }
+  };
 
   // ---- VEC: KV block prefetch registers (thread t: row t / CPR, channels
   //      8 (t % CPR) .. +7 of K and V) ----
@@ -196,7 +217,7 @@ bwd_dq_kernel(const BwdParams p) {
           rope_load4(tab, min(kvb + r, N - 1) + shift, D2, 4 * cc, cs);   // rows >= N are zero
         }
         rope_rotate8(xk, cs);
-        C::put8(&sK[r * LDK + 8 * cc], xk);
+        put_khat(r * LDK + 8 * cc, xk);
         if constexpr (std::is_same<IO, S>::value) {
           *reinterpret_cast<typename Raw8<IO>::vec*>(&sV[r * LDK + 8 * cc]) = pv[it].v;
         } else {
@@ -243,7 +264,7 @@ bwd_dq_kernel(const BwdParams p) {
         const int r = c / CPR, cc = c - r * CPR;
         if (c < rows * CPR) {
           rope_rotate8(xk[it], cs[it]);
-          C::put8(&sK[r * LDK + 8 * cc], xk[it]);
+          put_khat(r * LDK + 8 * cc, xk[it]);
           C::put8(&sV[r * LDK + 8 * cc], xv[it]);
           if constexpr (!TR) {
 #pragma unroll
@@ -281,6 +302,14 @@ bwd_dq_kernel(const BwdParams p) {
           const int kl = 32 * j + 8 * (lr >> 2) + 4 * h + (lr & 3);
           const Frag a = C::lds(&sK[kl * LDK + 32 * s + 8 * lg]);
           const Frag b = C::lds(&sV[kl * LDK + 32 * s + 8 * lg]);
+          if constexpr (PS) {
+            const Frag al = C::lds(&sKl[kl * LDK + 32 * s + 8 * lg]);
+#pragma unroll
+            for (int t = 0; t < QT; ++t) {
+              sacc[t][h] = C::mma(al, qf[t][s], sacc[t][h]);
+              sacc[t][h] = C::mma(a, qfl[t][s], sacc[t][h]);
+            }
+          }
 #pragma unroll
           for (int t = 0; t < QT; ++t) {
             sacc[t][h] = C::mma(a, qf[t][s], sacc[t][h]);
@@ -288,7 +317,7 @@ bwd_dq_kernel(const BwdParams p) {
           }
         }
       }
-      Frag dsf[QT];
+      Frag dsf[QT], dsfl[PS ? QT : 1];
 #pragma unroll
       for (int t = 0; t < QT; ++t) {
         float ds[8];
@@ -297,7 +326,10 @@ bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
           for (int i = 0; i < 4; ++i)
             ds[4 * h + i] = fast_exp2(__builtin_fmaf(sacc[t][h][i], p.scale_log2, -lse2[t])) * pacc[t][h][i];
-        dsf[t] = C::make(ds);
+        if constexpr (PS)
+          split_bf16x8(ds, dsf[t].v, dsfl[t].v);
+        else
+          dsf[t] = C::make(ds);
       }
 #pragma unroll
       for (int d = 0; d < DT; ++d) {
@@ -309,7 +341,10 @@ bwd_dq_kernel(const BwdParams p) {
         else
           a = C::lds(&sKt[(16 * d + lr) * LDT + 32 * j + 8 * lg]);
 #pragma unroll
-        for (int t = 0; t < QT; ++t) dqacc[t][d] = C::mma(a, dsf[t], dqacc[t][d]);
+        for (int t = 0; t < QT; ++t) {
+          if constexpr (PS) dqacc[t][d] = C::mma(a, dsfl[t], dqacc[t][d]);
+          dqacc[t][d] = C::mma(a, dsf[t], dqacc[t][d]);
+        }
       }
     }
   }
@@ -338,7 +373,9 @@ bwd_dq_kernel(const BwdParams p) {
 // computed, through buffer descriptors over the plane (rows >= N read 0), and
 // committed to LDS after the stage barrier.  Otherwise each stage is loaded
 // element-wise and synchronously.
-template <typename IO, int CT, int D, int NW, int KT, int QS, bool VEC>
+// PS (bf16 compute, head_dim >= 128): logits from split Q-hat (LDS, hi + lo)
+// and K-hat (registers, hi + lo), and dK-hat^T += Q-hat^T dS_hi + Q-hat^T dS_lo.
+template <typename IO, int CT, int D, int NW, int KT, int QS, bool VEC, bool PS>
 __global__ void __launch_bounds__(NW * 64)
 bwd_dkdv_kernel(const BwdParams p) {
   using C = Comp<CT>;
@@ -354,7 +391,9 @@ bwd_dkdv_kernel(const BwdParams p) {
   // (ds_read_b64_tr_b16); fp32 storage keeps explicit transposed copies.
   constexpr bool TR = sizeof(S) == 2;
 
+  static_assert(!PS || CT == DT_BF16, "split operands are bf16");
   __shared__ __attribute__((aligned(16))) S sQ[QS * LDQ];
+  __shared__ __attribute__((aligned(16))) S sQl[PS ? QS * LDQ : 8];   // PS: Q-hat lo
   __shared__ __attribute__((aligned(16))) S sQt[TR ? 8 : D * LDT];
   __shared__ __attribute__((aligned(16))) S sG[QS * LDQ];
   __shared__ __attribute__((aligned(16))) S sGt[TR ? 8 : D * LDT];
@@ -383,6 +422,7 @@ bwd_dkdv_kernel(const BwdParams p) {
 
   // ---- this wave's K-hat and V rows as B-operands ----
   Frag kf[KT][KS], vf[KT][KS];
+  Frag kfl[PS ? KT : 1][PS ? KS : 1];   // PS: K-hat lo
 #pragma unroll
   for (int u = 0; u < KT; ++u) {
     const int row = kv_first + 16 * u + lr;
@@ -400,7 +440,10 @@ bwd_dkdv_kernel(const BwdParams p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = y[e] = 0.f;
       }
-      kf[u][s] = C::make(x);
+      if constexpr (PS)
+        split_bf16x8(x, kf[u][s].v, kfl[u][s].v);
+      else
+        kf[u][s] = C::make(x);
       vf[u][s] = C::make(y);
     }
   }
@@ -410,6 +453,18 @@ bwd_dkdv_kernel(const BwdParams p) {
   for (int u = 0; u < KT; ++u)
 #pragma unroll
     for (int d = 0; d < DT; ++d) dvacc[u][d] = dkacc[u][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Q-hat row segment -> sQ (PS: hi to sQ, lo to sQl)
+  auto put_qhat = [&](int off, const float (&xq)[8]) __attribute__((always_inline)) {
+    if constexpr (PS) {
+      bf16x8 hi, lo;
+      split_bf16x8(xq, hi, lo);
+      *reinterpret_cast<bf16x8*>(&sQ[off]) = hi;
+      *reinterpret_cast<bf16x8*>(&sQl[off]) = lo;
+    } else {
+      C::put8(&sQ[off], xq);
+    }
+  };
 
   // ---- VEC: stage prefetch registers (thread t: row t / CPR, channels
   //      8 (t % CPR) .. +7 of Q and dO, their table row; threads t < QS: LSE
@@ -457,7 +512,7 @@ bwd_dkdv_kernel(const BwdParams p) {
         const float cs[8] = {pt[it][0][0], pt[it][0][1], pt[it][0][2], pt[it][0][3],
                              pt[it][1][0], pt[it][1][1], pt[it][1][2], pt[it][1][3]};
         rope_rotate8(xq, cs);
-        C::put8(&sQ[r * LDQ + 8 * cc], xq);
+        put_qhat(r * LDQ + 8 * cc, xq);
         C::put8(&sG[r * LDQ + 8 * cc], xg);
         if constexpr (!TR) {
 #pragma unroll
@@ -505,7 +560,7 @@ bwd_dkdv_kernel(const BwdParams p) {
         const int r = c / CPR, cc = c - r * CPR;
         if (c < rows * CPR) {
           rope_rotate8(xq[it], cs[it]);
-          C::put8(&sQ[r * LDQ + 8 * cc], xq[it]);
+          put_qhat(r * LDQ + 8 * cc, xq[it]);
           C::put8(&sG[r * LDQ + 8 * cc], xg[it]);
           if constexpr (!TR) {
 #pragma unroll
@@ -548,6 +603,11 @@ bwd_dkdv_kernel(const BwdParams p) {
             const int ql = 32 * j + 8 * (lr >> 2) + 4 * h + (lr & 3);
             const Frag a = C::lds(&sQ[ql * LDQ + 32 * s + 8 * lg]);
             const Frag b = C::lds(&sG[ql * LDQ + 32 * s + 8 * lg]);
+            if constexpr (PS) {
+              const Frag al = C::lds(&sQl[ql * LDQ + 32 * s + 8 * lg]);
+              sacc[h] = C::mma(al, kf[u][s], sacc[h]);
+              sacc[h] = C::mma(a, kfl[u][s], sacc[h]);
+            }
             sacc[h] = C::mma(a, kf[u][s], sacc[h]);
             pacc[h] = C::mma(b, vf[u][s], pacc[h]);
           }
@@ -564,7 +624,11 @@ bwd_dkdv_kernel(const BwdParams p) {
             dsv[e] = pr * (pacc[h][i] - dl[e]);
           }
         const Frag pf = C::make(pv);
-        const Frag dsf = C::make(dsv);
+        Frag dsf, dsfl;
+        if constexpr (PS)
+          split_bf16x8(dsv, dsf.v, dsfl.v);
+        else
+          dsf = C::make(dsv);
 #pragma unroll
         for (int d = 0; d < DT; ++d) {
           // A = dO^T / Q-hat^T rows 16d.., k-slot e <-> query 32j + 8lg + e (the P / dS order)
@@ -579,6 +643,7 @@ bwd_dkdv_kernel(const BwdParams p) {
             aq = C::lds(&sQt[(16 * d + lr) * LDT + 32 * j + 8 * lg]);
           }
           dvacc[u][d] = C::mma(ag, pf, dvacc[u][d]);
+          if constexpr (PS) dkacc[u][d] = C::mma(aq, dsfl, dkacc[u][d]);
           dkacc[u][d] = C::mma(aq, dsf, dkacc[u][d]);
         }
       }
@@ -722,25 +787,26 @@ hipError_t launch_bwd_pre(const BwdParams& p, int io, int D, hipStream_t st) {
 template <typename IO, int CT, int D>
 static hipError_t dq_launch(const BwdParams& p0, bool write_delta, hipStream_t st) {
   using SH = BwdShape<D, CT == DT_F32>;
+  constexpr bool PS = precise_logits(CT, D);
   BwdParams p = p0;
   const int grid = p.n_wg = p.B * p.H * p.n_blk;
   // (fp32 compute has no registers to spare for the prefetch)
   if constexpr (CT != DT_F32) {
     if (p.vec_k && p.vec_v) {
       if (write_delta)
-        hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, true, true>),
+        hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, true, true, PS>),
                            dim3(grid), dim3(SH::DQ_NW * 64), 0, st, p);
       else
-        hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, false, true>),
+        hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, false, true, PS>),
                            dim3(grid), dim3(SH::DQ_NW * 64), 0, st, p);
       return hipGetLastError();
     }
   }
   if (write_delta)
-    hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, true, false>),
+    hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, true, false, PS>),
                        dim3(grid), dim3(SH::DQ_NW * 64), 0, st, p);
   else
-    hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, false, false>),
+    hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, false, false, PS>),
                        dim3(grid), dim3(SH::DQ_NW * 64), 0, st, p);
   return hipGetLastError();
 }
@@ -748,17 +814,18 @@ static hipError_t dq_launch(const BwdParams& p0, bool write_delta, hipStream_t s
 template <typename IO, int CT, int D>
 static hipError_t dkdv_launch(const BwdParams& p0, hipStream_t st) {
   using SH = BwdShape<D, CT == DT_F32>;
+  constexpr bool PS = precise_logits(CT, D);
   BwdParams p = p0;
   const int grid = p.n_wg = p.B * p.H * p.n_blk;
   // (fp32 compute has no registers to spare for the prefetch)
   if constexpr (CT != DT_F32) {
     if (p.vec_q && p.vec_do) {
-      hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS, true>), dim3(grid),
+      hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS, true, PS>), dim3(grid),
                          dim3(SH::KV_NW * 64), 0, st, p);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS, false>), dim3(grid),
+  hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS, false, PS>), dim3(grid),
                      dim3(SH::KV_NW * 64), 0, st, p);
   return hipGetLastError();
 }

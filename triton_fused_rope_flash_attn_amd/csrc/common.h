@@ -387,6 +387,22 @@ template <> struct Comp<DT_F32> {
 };
 
 // ---------------------------------------------------------------------------
+// Split bf16 operands (bf16 compute, "precise" products): x = hi + lo with
+// hi = bf16(x) and lo = bf16(x - hi), about 16 significant bits between them.
+// A product a.b is then taken as a_hi.b_hi + a_lo.b_hi + a_hi.b_lo (the
+// dropped a_lo.b_lo is below the fp32 accumulation error); with one operand
+// split only, as a_hi.b_hi + a_hi.b_lo.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void split_bf16x8(const float (&x)[8], bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const bf16 h = (bf16)x[e];
+    hi[e] = h;
+    lo[e] = (bf16)(x[e] - (float)h);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Misc.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -79,7 +79,11 @@ constexpr float kRescaleSlack = 8.0f;   // log2 units: P <= 2^8 between rescales
 
 // VEC: every tensor of the call allows 16-byte vector access (decided on the
 // host); the generic instantiation gathers element by element instead.
-template <typename IO, int CT, int D, int NW, int QT, int KC, int TABROWS, bool VEC>
+// PS (bf16 compute): the logits are taken from split operands, K-hat = hi + lo
+// (two LDS tiles) and Q-hat = hi + lo (registers), as hi.hi + lo.hi + hi.lo:
+// the rounding of the rotated rows to bf16 is what dominates the error of
+// bf16 attention at long, wide planes, and it no longer enters S.
+template <typename IO, int CT, int D, int NW, int QT, int KC, int TABROWS, bool VEC, bool PS>
 __global__ void __launch_bounds__(NW * 64)
 fwd_kernel(const FwdParams p) {
   using C = Comp<CT>;
@@ -108,7 +112,9 @@ fwd_kernel(const FwdParams p) {
   // row-major and each V^T fragment is gathered element by element (VROW).
   constexpr bool TRV = sizeof(S) == 2;
   constexpr bool VROW = !TRV && D >= 256;
+  static_assert(!PS || CT == DT_BF16, "split operands are bf16");
   __shared__ __attribute__((aligned(16))) S sK[2][KC * LDK];
+  __shared__ __attribute__((aligned(16))) S sKl[2][PS ? KC * LDK : 8];   // PS: K-hat lo
   __shared__ __attribute__((aligned(16))) S sVt[2][(TRV || VROW) ? KC * LDK : D * LDV];
   // LDS copy of the packed table: D/2 (cos, sin) pairs = D floats per row,
   // 16-byte chunk c of row r stored at chunk c ^ (r & (D/4 - 1)) (bank-spread
@@ -273,7 +279,14 @@ fwd_kernel(const FwdParams p) {
           } else {
             rope_rotate8(xk, pcs[it][x]);
           }
-          C::put8(&sK[slot][kperm(2 * rp + x) * LDK + 8 * cc], xk);
+          if constexpr (PS) {
+            bf16x8 hi, lo;
+            split_bf16x8(xk, hi, lo);
+            *reinterpret_cast<bf16x8*>(&sK[slot][kperm(2 * rp + x) * LDK + 8 * cc]) = hi;
+            *reinterpret_cast<bf16x8*>(&sKl[slot][kperm(2 * rp + x) * LDK + 8 * cc]) = lo;
+          } else {
+            C::put8(&sK[slot][kperm(2 * rp + x) * LDK + 8 * cc], xk);
+          }
           if constexpr (TRV || VROW) {
             S* dst = &sVt[slot][(2 * rp + x) * LDK + 8 * cc];
             if constexpr (std::is_same<IO, S>::value) {
@@ -333,6 +346,7 @@ fwd_kernel(const FwdParams p) {
     }
   };
   Frag qf[QT][KS];
+  Frag qfl[PS ? QT : 1][PS ? KS : 1];   // PS: Q-hat lo
   auto commit_q = [&](int qb) __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < QT; ++t)
@@ -348,7 +362,10 @@ fwd_kernel(const FwdParams p) {
         } else {
           rope_rotate8(x, qcs[t][s]);
         }
-        qf[t][s] = C::make(x);
+        if constexpr (PS)
+          split_bf16x8(x, qf[t][s].v, qfl[t][s].v);
+        else
+          qf[t][s] = C::make(x);
       }
   };
 
@@ -538,33 +555,45 @@ fwd_kernel(const FwdParams p) {
   // Without the LDS table (D = 128 or long planes), or with 32-bit I/O (twice
   // the prefetch registers), the registers of the pipeline are not free: the
   // same work block by block.
-  constexpr bool kPipe = kTabLds && sizeof(IO) == 2;
+  constexpr bool kPipe = kTabLds && sizeof(IO) == 2 && !PS;
   // One KV chunk for all QT subtiles of the wave.  Subtiles past the last
   // query row hold zero rows and are computed anyway: every wave of a
   // workgroup then runs the same instruction stream with no per-subtile
   // guards, and for the 16-row-ragged N of ViT planes the extra work lands on
   // SIMDs that would otherwise wait at the next barrier.
-  // One 32-key block for all QT subtiles of the wave.  Subtiles past the last
-  // query row hold zero rows and are computed anyway: every wave of a
+  // One 32-key block for all QT subtiles of the wave, in two halves so that a
+  // chunk can software-pipeline them: blk_logits issues the S^T products of a
+  // block, blk_out its online softmax and O^T += V^T P^T.  Subtiles past the
+  // last query row hold zero rows and are computed anyway: every wave of a
   // workgroup then runs the same instruction stream with no per-subtile
-  // guards, and for the 16-row-ragged N of ViT planes the extra work lands on
-  // SIMDs that would otherwise wait at the next barrier.  MASKED: the block
-  // holding key N-1 (keys >= N get probability 0).
-  auto block = [&](auto maskc, const S* __restrict__ cK, const S* __restrict__ cV, int kvb, int j) __attribute__((always_inline)) {
-    constexpr bool MASKED = decltype(maskc)::value;
+  // guards.  MASKED: the block holding key N-1 (keys >= N get probability 0).
+  auto blk_logits = [&](const S* __restrict__ cK, const S* __restrict__ cKl, int j, SAcc& sacc)
+      __attribute__((always_inline)) {
     // ---- S^T = K-hat Q-hat^T for 32 keys (each K-hat fragment feeds QT MFMAs) ----
-    f32x4 sacc[QT][2];
 #pragma unroll
     for (int t = 0; t < QT; ++t) sacc[t][0] = sacc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const Frag a = C::lds(&cK[(32 * j + 16 * h + lr) * LDK + 32 * s + 8 * lg]);
+        const int off = (32 * j + 16 * h + lr) * LDK + 32 * s + 8 * lg;
+        const Frag a = C::lds(&cK[off]);
+        if constexpr (PS) {
+          const Frag al = C::lds(&cKl[off]);
+#pragma unroll
+          for (int t = 0; t < QT; ++t) {
+            sacc[t][h] = C::mma(al, qf[t][s], sacc[t][h]);
+            sacc[t][h] = C::mma(a, qfl[t][s], sacc[t][h]);
+          }
+        }
 #pragma unroll
         for (int t = 0; t < QT; ++t) sacc[t][h] = C::mma(a, qf[t][s], sacc[t][h]);
       }
     }
+  };
+  auto blk_out = [&](auto maskc, const S* __restrict__ cV, int kvb, int j, const SAcc& sacc)
+      __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(maskc)::value;
     // ---- online softmax; lane holds keys kvb + 32j + 8lg + (0..7) of its row ----
     const int lim = N - (kvb + 32 * j + 8 * lg);   // keys e < lim are valid (MASKED only)
     Frag pf[QT];
@@ -617,12 +646,44 @@ fwd_kernel(const FwdParams p) {
       for (int t = 0; t < QT; ++t) oacc[t][d] = C::mma(a, pf[t], oacc[t][d]);
     }
   };
-  // One KV chunk: full blocks, then the block holding key N-1 if it is ragged.
-  auto chunk_serial = [&](const S* __restrict__ cK, const S* __restrict__ cV, int kvb) __attribute__((always_inline)) {
+  // One KV chunk of nb blocks (the last one ragged when N - kvb < KC and not
+  // a multiple of 32).  With one subtile per wave the logits of block j+1 are
+  // issued before the softmax of block j, so that those MFMAs (three per
+  // product with split operands) run while the VALU computes block j's
+  // probabilities; two blocks per trip alternate the two logit accumulators
+  // without copies.
+  auto chunk_serial = [&](const S* __restrict__ cK, const S* __restrict__ cKl, const S* __restrict__ cV,
+                          int kvb) __attribute__((always_inline)) {
     const int nkeys = min(KC, N - kvb);
-    const int nfull = nkeys / 32;
-    for (int j = 0; j < nfull; ++j) block(std::false_type{}, cK, cV, kvb, j);
-    if (nkeys % 32) block(std::true_type{}, cK, cV, kvb, nfull);
+    if constexpr (QT == 1 && sizeof(S) == 2) {
+      // every block goes through the masked softmax (a key limit past the
+      // block for full ones): one inlined copy per call site keeps the
+      // pipelined loop within the register budget
+      const int nb = (nkeys + 31) >> 5;
+      SAcc sA, sB;
+      blk_logits(cK, cKl, 0, sA);
+      int j = 0;
+      for (; j + 1 < nb; j += 2) {
+        blk_logits(cK, cKl, j + 1, sB);
+        blk_out(std::true_type{}, cV, kvb, j, sA);
+        if (j + 2 < nb) blk_logits(cK, cKl, j + 2, sA);
+        blk_out(std::true_type{}, cV, kvb, j + 1, sB);
+      }
+      if (j < nb) blk_out(std::true_type{}, cV, kvb, j, sA);   // odd block count: last logits in sA
+    } else {
+      // two subtiles per wave, or fp32 compute (split operands): two blocks'
+      // logits do not fit beside their accumulators, so block by block
+      const int nfull = nkeys / 32;
+      SAcc sA;
+      for (int j = 0; j < nfull; ++j) {
+        blk_logits(cK, cKl, j, sA);
+        blk_out(std::false_type{}, cV, kvb, j, sA);
+      }
+      if (nkeys % 32) {
+        blk_logits(cK, cKl, nfull, sA);
+        blk_out(std::true_type{}, cV, kvb, nfull, sA);
+      }
+    }
   };
 
   int it = 0;
@@ -739,7 +800,7 @@ fwd_kernel(const FwdParams p) {
       } else {
         mem();
         lds_barrier();
-        if (nt > 0) chunk_serial(sK[slot], sVt[slot], chunk_start(c));
+        if (nt > 0) chunk_serial(sK[slot], sKl[PS ? slot : 0], sVt[slot], chunk_start(c));
       }
       ++g;
     };
@@ -844,12 +905,15 @@ static hipError_t fwd_launch(const FwdParams& p0, hipStream_t st) {
   FwdParams p = p0;
   // fp32 compute keeps 4-byte tiles in LDS: no room for the table copy there
   constexpr int TR = CT == DT_F32 ? 0 : SH::TABROWS;
+  // split-operand logits for bf16 compute at head_dim >= 128 (the backward's
+  // split kernels use the same rule, so both passes see the same S)
+  constexpr bool PS = precise_logits(CT, D);
   const bool tab = TR > 0 && p.N + 1 - p.has_cls <= TR;
   const bool vec = p.vec_q && p.vec_k && p.vec_v && p.vec_o;
-  auto kern = tab ? (vec ? fwd_kernel<IO, CT, D, SH::NW, SH::QT, SH::KC, TR, true>
-                         : fwd_kernel<IO, CT, D, SH::NW, SH::QT, SH::KC, TR, false>)
-                  : (vec ? fwd_kernel<IO, CT, D, SH::NW, SH::QT, SH::KC, 0, true>
-                         : fwd_kernel<IO, CT, D, SH::NW, SH::QT, SH::KC, 0, false>);
+  auto kern = tab ? (vec ? fwd_kernel<IO, CT, D, SH::NW, SH::QT, SH::KC, TR, true, PS>
+                         : fwd_kernel<IO, CT, D, SH::NW, SH::QT, SH::KC, TR, false, PS>)
+                  : (vec ? fwd_kernel<IO, CT, D, SH::NW, SH::QT, SH::KC, 0, true, PS>
+                         : fwd_kernel<IO, CT, D, SH::NW, SH::QT, SH::KC, 0, false, PS>);
   const int grid = persistent_grid(reinterpret_cast<const void*>(kern), SH::NW * 64, p.n_items);
   if (grid <= 0) return hipErrorInvalidConfiguration;
   p.n_wg = grid;

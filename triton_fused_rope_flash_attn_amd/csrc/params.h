@@ -64,6 +64,13 @@ hipError_t launch_rope_pack(const float* cosp, int64_t cs0, int64_t cs1, const f
                             int64_t ss0, int64_t ss1, int n_pos, int d2, float* out,
                             hipStream_t st);
 
+// Split-operand ("precise") logits and dS: bf16 compute at head_dim >= 128.
+// Rounding the rotated Q / K rows to bf16 before the logits product is the
+// dominant error of bf16 attention there (long, wide planes with large
+// logits); fp16 compute keeps 3 more mantissa bits and fp32 compute splits
+// every operand anyway.
+constexpr bool precise_logits(int ct, int D) { return ct == 2 /* DT_BF16 */ && D >= 128; }
+
 // Workgroups for a persistent kernel: min(items, CUs x resident workgroups per
 // CU), with `dyn_lds` bytes of dynamic LDS per workgroup; <= 0 on a HIP error.
 int persistent_grid(const void* kernel, int block_threads, int items, size_t dyn_lds = 0);
