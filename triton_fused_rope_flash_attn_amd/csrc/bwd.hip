@@ -155,6 +155,7 @@ bwd_dq_kernel(const BwdParams p) {
     lse2[t] = row < N ? p.lse[prow + row] * kLog2e : 0.f;
   }
   const bool wave_active = qblk * QROWS + wave * QT * 16 < N;
+  const float dq_scale = p.scale / p.scale_log2;   // K-hat is staged pre-scaled by scale * log2(e)
 
   f32x4 dqacc[QT][DT];
 #pragma unroll
@@ -162,8 +163,12 @@ bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
     for (int d = 0; d < DT; ++d) dqacc[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // K-hat row segment -> sK (PS: hi to sK, lo to sKl)
-  auto put_khat = [&](int off, const float (&xk)[8]) __attribute__((always_inline)) {
+  // K-hat row segment -> sK (PS: hi to sK, lo to sKl), pre-scaled by
+  // softmax_scale * log2(e) as in the forward pass, so that both passes see
+  // bit-identical logits in log2 units (dQ's scale divides it out again)
+  auto put_khat = [&](int off, float (&xk)[8]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xk[e] *= p.scale_log2;
     if constexpr (PS) {
       bf16x8 hi, lo;
       split_bf16x8(xk, hi, lo);
@@ -325,7 +330,7 @@ bwd_dq_kernel(const BwdParams p) {
         for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            ds[4 * h + i] = fast_exp2(__builtin_fmaf(sacc[t][h][i], p.scale_log2, -lse2[t])) * pacc[t][h][i];
+            ds[4 * h + i] = fast_exp2(sacc[t][h][i] - lse2[t]) * pacc[t][h][i];
         if constexpr (PS)
           split_bf16x8(ds, dsf[t].v, dsfl[t].v);
         else
@@ -357,7 +362,7 @@ bwd_dq_kernel(const BwdParams p) {
       for (int d = 0; d < DT; ++d) {
         float g4[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) g4[r] = dqacc[t][d][r] * p.scale;
+        for (int r = 0; r < 4; ++r) g4[r] = dqacc[t][d][r] * dq_scale;
         rope_unrotate4(g4, tab, row + shift, D2, 8 * d + 2 * lg);
         store4(dQ + row * p.sdq[2] + (16 * d + 4 * lg) * p.sdq[3], p.sdq[3], p.vec_dq, g4);
       }
@@ -435,6 +440,9 @@ bwd_dkdv_kernel(const BwdParams p) {
         float cs[8];
         rope_load4(tab, row + shift, D2, c0 / 2, cs);
         rope_rotate8(x, cs);
+        // pre-scaled by softmax_scale * log2(e), as every kernel stages K-hat
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] *= p.scale_log2;
         load8(V + row * p.sv[2] + c0 * p.sv[3], p.sv[3], p.vec_v, y);
       } else {
 #pragma unroll
@@ -619,7 +627,7 @@ bwd_dkdv_kernel(const BwdParams p) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int e = 4 * h + i;
-            const float pr = kvalid ? fast_exp2(sacc[h][i] * p.scale_log2 - l2[e]) : 0.f;
+            const float pr = kvalid ? fast_exp2(sacc[h][i] - l2[e]) : 0.f;
             pv[e] = pr;
             dsv[e] = pr * (pacc[h][i] - dl[e]);
           }

@@ -15,7 +15,7 @@
 // dQ-hat^T = K-hat^T dS^T is read transposed.  The plane's queries are swept in
 // stages of 32 rows, double-buffered in LDS, one barrier per stage:
 //   commit   staged registers -> LDS: Q-hat and dO rows (row-major),
-//            LSE*log2(e), -delta = -rowsum(dO*O)
+//            -LSE*log2(e), -delta = -rowsum(dO*O)
 //   barrier
 //   prefetch next stage's Q, dO, O rows (+ RoPE table rows, LSE)
 //   dQ of the previous stage: dQ-hat^T = K-hat^T dS^T from the resident
@@ -207,7 +207,8 @@ bwd_plane_kernel(const BwdParams p) {
       const float d = dpp_sum8(dot8(pg, po, 0.f));
       if (sc == 0) sDl[buf][sr] = -d;   // stored negated: it seeds the dP accumulators
     } else if (t - 256 < QS) {
-      sL2[buf][t - 256] = qb + (t - 256) < N ? plse * kLog2e : INFINITY;
+      // -LSE in log2 units seeds the logit accumulators (rows >= N: -inf, so P = 0)
+      sL2[buf][t - 256] = qb + (t - 256) < N ? -plse * kLog2e : -INFINITY;
     }
   };
 
@@ -268,6 +269,10 @@ bwd_plane_kernel(const BwdParams p) {
         unpack8(rk[u][s], x);
         unpack8(rv[u][s], y);
         rope_rotate8(x, cs);
+        // K-hat pre-scaled by softmax_scale * log2(e): the logits product then
+        // yields S in log2 units directly (dQ's scale divides it out again)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] *= c2;
         kf[u][s] = C::make(x);
         vf[u][s] = C::make(y);
         // materialise V here (for 16-bit I/O the conversion folds away and the
@@ -280,14 +285,8 @@ bwd_plane_kernel(const BwdParams p) {
     }
   };
 
-  // S-accumulator start per own subtile: 0 for keys < N, -inf beyond (all 4
-  // rows of the lane's column are the same key)
-  f32x4 kmask[2];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const float m = kw + 16 * u + lr < N ? 0.f : -INFINITY;
-    kmask[u] = f32x4{m, m, m, m};
-  }
+  // dQ-hat = dS K-hat * scale with K-hat stored pre-scaled by c2
+  const float dq_scale = p.scale / c2;
 
   f32x4 dvacc[2][4], dkacc[2][4];
 
@@ -349,7 +348,7 @@ bwd_plane_kernel(const BwdParams p) {
       const f32x4 t = tab_chunk(sTab, trow, 4 * dd + lg);   // pairs 8dd + 2lg + (0, 1)
 #pragma unroll
       for (int r = 0; r < 2; ++r) {   // g = R^T g-hat
-        const float e = acc[2 * r] * p.scale, o = acc[2 * r + 1] * p.scale;
+        const float e = acc[2 * r] * dq_scale, o = acc[2 * r + 1] * dq_scale;
         const float c = t[2 * r], sn = t[2 * r + 1];
         g4[2 * r] = e * c + o * sn;
         g4[2 * r + 1] = o * c - e * sn;
@@ -370,10 +369,12 @@ bwd_plane_kernel(const BwdParams p) {
     }
   };
   // ---- S, dP, P, dS, dV, dK for the wave's two subtiles over one 32-query
-  //      stage (query rows in natural order, see above).  A wave whose second
-  //      subtile has no key < N sweeps it too: its S accumulators start at
-  //      -inf and its K / V rows are zero, so P = dS = 0 there and its dK / dV
-  //      accumulators stay 0.  One code path for every active wave keeps the
+  //      stage (query rows in natural order, see above).  Keys >= N (the rest
+  //      of the subtile holding key N-1, and all of a subtile past it) need no
+  //      mask: their K-hat and V rows are zero, so S = dP = 0 there and P, dS
+  //      are finite (P is clamped to [0, 1], which the exact P never leaves);
+  //      their dS^T rows meet zero K-hat rows in the dQ products and their dK /
+  //      dV rows are never stored.  One code path for every active wave keeps the
   //      dK / dV accumulators in the same registers across stages (a per-wave
   //      choice between sweep variants makes the compiler copy all of them at
   //      the join every stage), and a wave with one live subtile shares its
@@ -388,14 +389,15 @@ bwd_plane_kernel(const BwdParams p) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int q0 = 16 * h + 4 * lg;   // queries q0 .. q0+3 in this lane
-        const f32x4 l2 = *reinterpret_cast<const f32x4*>(&sL2[buf][q0]);
+        const f32x4 nl2 = *reinterpret_cast<const f32x4*>(&sL2[buf][q0]);   // -LSE * log2(e)
         const f32x4 ndl = *reinterpret_cast<const f32x4*>(&sDl[buf][q0]);   // -delta
-        // accumulators start at the key mask (S) and at -delta (dP), so that
-        // P = exp2(S*c2 - l2) is 0 for keys >= N and dP - delta needs no extra op
+        // accumulators start at -LSE (S, in log2 units through the pre-scaled
+        // K-hat) and at -delta (dP): P = exp2(acc) and dP - delta need no
+        // further arithmetic
         f32x4 sacc[NUA], pacc[NUA];
 #pragma unroll
         for (int u = 0; u < NUA; ++u) {
-          sacc[u] = kmask[u];
+          sacc[u] = nl2;
           pacc[u] = ndl;
         }
         const int qr = 16 * h + lr;
@@ -413,7 +415,7 @@ bwd_plane_kernel(const BwdParams p) {
         for (int u = 0; u < NUA; ++u) {
           float pv[4], dsv[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) pv[i] = fast_exp2(__builtin_fmaf(sacc[u][i], c2, -l2[i]));
+          for (int i = 0; i < 4; ++i) pv[i] = __builtin_amdgcn_fmed3f(fast_exp2(sacc[u][i]), 0.f, 1.f);
 #pragma unroll
           for (int i = 0; i < 4; ++i) dsv[i] = pv[i] * pacc[u][i];
           C::set2(pf[u], 2 * h, pv[0], pv[1]);

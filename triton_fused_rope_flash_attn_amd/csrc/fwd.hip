@@ -279,6 +279,11 @@ fwd_kernel(const FwdParams p) {
           } else {
             rope_rotate8(xk, pcs[it][x]);
           }
+          // K-hat pre-scaled by softmax_scale * log2(e): the logits come out
+          // of the MFMAs in log2 units (every kernel stages K-hat this way, so
+          // the forward and backward passes see bit-identical logits)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) xk[e] *= c2;
           if constexpr (PS) {
             bf16x8 hi, lo;
             split_bf16x8(xk, hi, lo);
@@ -427,14 +432,14 @@ fwd_kernel(const FwdParams p) {
   // block for its query row.  MASKED: keys e >= lim get probability 0.
   // The running max only has to bound the exponent: O and the row sum are
   // rescaled (group max, times 2^(m_old - m_new)) only when some lane's own
-  // max exceeds m_run + slack; m_thr = (m_run + slack) / c2 in logit units.
+  // max exceeds m_thr = m_run + slack (logits, m_run and m_thr are all in
+  // log2 units through the pre-scaled K-hat).
   //
   // The common case has no branch: soft() computes P with the current
   // running max and reports whether any row crossed its threshold; only then
   // does fixup() rescale and recompute the block (rare after an item's first
   // block).  Straight-line code lets the scheduler interleave these VALU
   // instructions with the MFMAs of the neighbouring blocks.
-  const float inv_c2 = 1.f / c2;
   auto block_vals = [&](auto maskc, const SAcc& sa, int t, int lim, float (&sv)[8]) __attribute__((always_inline)) {
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -452,7 +457,7 @@ fwd_kernel(const FwdParams p) {
     float pv8[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      pv8[e] = fast_exp2(__builtin_fmaf(sv[e], c2, -m_run[t]));
+      pv8[e] = fast_exp2(sv[e] - m_run[t]);
       l_run[t] += pv8[e];
     }
     pft = C::make(pv8);
@@ -474,14 +479,14 @@ fwd_kernel(const FwdParams p) {
     for (int t = 0; t < QT; ++t) {
       float sv[8];
       block_vals(maskc, sa, t, lim, sv);
-      const float mx = group4_max(max8(sv)) * c2;
+      const float mx = group4_max(max8(sv));
       const float mnew = fmaxf(m_run[t], mx);
       const float alpha = fast_exp2(m_run[t] - mnew);
       l_run[t] = lkeep[t] * alpha;
 #pragma unroll
       for (int d = 0; d < DT; ++d) oacc[t][d] *= alpha;
       m_run[t] = mnew;
-      m_thr[t] = (mnew + kRescaleSlack) * inv_c2;
+      m_thr[t] = mnew + kRescaleSlack;
       probs(sv, t, pf[t]);
     }
   };
@@ -610,23 +615,23 @@ fwd_kernel(const FwdParams p) {
       }
       // The running max only has to bound the exponent: rescale (group max,
       // O and row sum times 2^(m_old - m_new)) only when some lane's own max
-      // exceeds m_run + slack; m_thr = (m_run + slack) / c2 in logit units.
+      // exceeds m_thr = m_run + slack (log2 units).
       const float ml = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
                              fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
       if (__any(ml > m_thr[t])) {
-        const float mx = group4_max(ml) * c2;
+        const float mx = group4_max(ml);
         const float mnew = fmaxf(m_run[t], mx);
         const float alpha = fast_exp2(m_run[t] - mnew);
         l_run[t] *= alpha;
 #pragma unroll
         for (int d = 0; d < DT; ++d) oacc[t][d] *= alpha;
         m_run[t] = mnew;
-        m_thr[t] = (mnew + kRescaleSlack) * inv_c2;
+        m_thr[t] = mnew + kRescaleSlack;
       }
       float pv8[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        pv8[e] = fast_exp2(__builtin_fmaf(sv[e], c2, -m_run[t]));
+        pv8[e] = fast_exp2(sv[e] - m_run[t]);
         l_run[t] += pv8[e];
       }
       pf[t] = C::make(pv8);
