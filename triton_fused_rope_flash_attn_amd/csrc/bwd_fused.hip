@@ -323,8 +323,8 @@ bwd_plane_kernel(const BwdParams p) {
   // whole kernel: per stage only the buffer base changes
   const int dqr0 = 8 * lg + (lr >> 2);
   const int dqo0 = sw32(dqr0, 16 * qt + 4 * (lr & 3)), dqo1 = sw32(dqr0 + 4, 16 * qt + 4 * (lr & 3));
-  auto dq = [&](int plane, __amdgpu_buffer_rsrc_t rdq, int sp) __attribute__((always_inline)) {
-    const int buf = sp & 1;
+  // (buf = sp & 1; a compile-time constant inside the stage loop)
+  auto dq = [&](int plane, __amdgpu_buffer_rsrc_t rdq, int sp, int buf) __attribute__((always_inline)) {
     const int qb = sp * QS;
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
     const S* db0 = &sdS[buf][dqo0];
@@ -486,10 +486,15 @@ bwd_plane_kernel(const BwdParams p) {
 #pragma unroll
       for (int d = 0; d < 4; ++d) dvacc[u][d] = dkacc[u][d] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int st = 0; st < nstages; ++st) {
-      const int buf = st & 1;
+    // One query stage.  The stage loop runs two stages per trip, so the LDS
+    // buffer index BUF is a compile-time constant and the buffers' addresses
+    // fold into the LDS instructions' offsets.  FIRST: stage 0 (already
+    // committed above, no dQ of a previous stage).
+    auto stage = [&](int st, auto bufc, auto firstc) __attribute__((always_inline)) {
+      constexpr int buf = decltype(bufc)::value;
+      constexpr bool FIRST = decltype(firstc)::value;
       const int qb = st * QS;
-      if (st > 0) {
+      if constexpr (!FIRST) {
         commit(buf, qb);
         lds_barrier();
       }
@@ -503,15 +508,24 @@ bwd_plane_kernel(const BwdParams p) {
         if (last) rs = stage_rs(tp);
         prefetch(tp, rs, last ? 0 : qb + QS);
       }
-      if (st > 0) dq(plane, rdq, st - 1);
+      if constexpr (!FIRST) dq(plane, rdq, st - 1, buf ^ 1);
       if (nu > 0) sweep_keys(buf);
+    };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    stage(0, B0{}, std::true_type{});
+    int st = 1;
+    for (; st + 1 < nstages; st += 2) {
+      stage(st, B1{}, std::false_type{});
+      stage(st + 1, B0{}, std::false_type{});
     }
+    if (st < nstages) stage(st, B1{}, std::false_type{});
 
     // kf / vf are dead: start the next plane's own K / V rows, then finish this
     // plane: dQ of the last stage, dK / dV
     prefetch_kv(nxt >= 0 ? nxt : plane);
     lds_barrier();
-    dq(plane, rdq, nstages - 1);
+    dq(plane, rdq, nstages - 1, (nstages - 1) & 1);
     // ---- dK / dV epilogue: lane holds dV /
     //      dK-hat of key kw + 16u + lr, channels 16d + 4lg + (0..3) ----
     if constexpr (VEC && sizeof(IO) == 2) {
