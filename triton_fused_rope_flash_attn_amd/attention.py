@@ -151,6 +151,9 @@ def _fwd_setup_context(ctx, inputs, output):
     q, k, v, rope, n_pos, has_cls, softmax_scale, compute_dtype = inputs
     o, lse = output
     ctx.mark_non_differentiable(lse)
+    # LSE's incoming gradient is never used: without this, autograd fills a
+    # zero tensor for it on every backward (an extra kernel per step)
+    ctx.set_materialize_grads(False)
     ctx.save_for_backward(q, k, v, o, lse, rope)
     ctx.n_pos = n_pos
     ctx.has_cls = has_cls
@@ -159,6 +162,8 @@ def _fwd_setup_context(ctx, inputs, output):
 
 
 def _fwd_backward(ctx, do, _dlse):
+    if do is None:   # O received no gradient (grads are not materialised)
+        return None, None, None, None, None, None, None, None
     q, k, v, o, lse, rope = ctx.saved_tensors
     dq, dk, dv = attn_bwd(do, q, k, v, o, lse, rope, ctx.n_pos, ctx.has_cls,
                           ctx.softmax_scale, ctx.compute_dtype)
