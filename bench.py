@@ -338,8 +338,8 @@ def profile_run(wl, steps, warmup):
     prewarm(lambda: torch.mm(a, b))
     del a, b
     for _ in range(warmup + steps):
-        o, lse = torch.ops.farope.attn_fwd(q, k, v, rope, n_pos, wl["has_cls"], scale, _lib.BF16)
-        torch.ops.farope.attn_bwd(do, q, k, v, o, lse, rope, n_pos, wl["has_cls"], scale, _lib.BF16)
+        o, lse, res = torch.ops.farope.attn_fwd(q, k, v, rope, n_pos, wl["has_cls"], scale, _lib.BF16)
+        torch.ops.farope.attn_bwd(do, q, k, v, o, lse, rope, n_pos, wl["has_cls"], scale, _lib.BF16, res)
     # calibration: a plain copy reads and writes exactly 256 MiB each
     src = torch.empty(128 * 1024 * 1024, dtype=torch.bfloat16, device="cuda").fill_(1.0)
     dst = torch.empty_like(src)
@@ -412,16 +412,16 @@ def main():
     rope = table.packed()
     scale = 1.0 / math.sqrt(D)
     n_pos = N - int(wl["has_cls"])
-    o, lse = torch.ops.farope.attn_fwd(q, k, v, rope, n_pos, wl["has_cls"], scale, _lib.BF16)
+    o, lse, res = torch.ops.farope.attn_fwd(q, k, v, rope, n_pos, wl["has_cls"], scale, _lib.BF16)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
            torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     for _ in range(3):
-        torch.ops.farope.attn_bwd(do, q, k, v, o, lse, rope, n_pos, wl["has_cls"], scale, _lib.BF16)
+        torch.ops.farope.attn_bwd(do, q, k, v, o, lse, rope, n_pos, wl["has_cls"], scale, _lib.BF16, res)
     for a, b, c in ev:
         a.record(stream)
-        o, lse = torch.ops.farope.attn_fwd(q, k, v, rope, n_pos, wl["has_cls"], scale, _lib.BF16)
+        o, lse, res = torch.ops.farope.attn_fwd(q, k, v, rope, n_pos, wl["has_cls"], scale, _lib.BF16)
         b.record(stream)
-        torch.ops.farope.attn_bwd(do, q, k, v, o, lse, rope, n_pos, wl["has_cls"], scale, _lib.BF16)
+        torch.ops.farope.attn_bwd(do, q, k, v, o, lse, rope, n_pos, wl["has_cls"], scale, _lib.BF16, res)
         c.record(stream)
     torch.cuda.synchronize()
     t_fwd = statistics.mean(a.elapsed_time(b) for a, b, c in ev) * 1e-3

@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define FAROPE_ABI_VERSION 1
+#define FAROPE_ABI_VERSION 2
 
 typedef enum farope_dtype {
   FAROPE_F32 = 0,
@@ -84,22 +84,35 @@ int farope_rope_pack(const float* cosp, int64_t cos_stride0, int64_t cos_stride1
                      int32_t n_pos, int32_t d2, float* packed, void* stream);
 
 /*
+ * Elements of the optional O residual buffer (o_res) a call uses:
+ * batch * heads * seq_len * head_dim for bf16 tensors computed in bf16 at
+ * head_dim >= 128, else 0.  Those calls take the logits from split bf16
+ * operands; what then limits dQ / dK is delta = rowsum(dout * o) computed
+ * from the bf16-rounded o, so the forward can also store o's rounding
+ * residual bf16(o - bf16(o)) in a contiguous [B, H, N, D] buffer of the I/O
+ * dtype, and the backward adds it to o for delta.  No counterpart in the
+ * reference (whose delta uses the stored o, FA:352-354).
+ */
+size_t farope_attn_residual_elems(const farope_attn_desc* desc);
+
+/*
  * Forward: o = softmax(scale * (R q)(R k)^T) v, lse = logsumexp of the
  * scaled logits per row (natural log).  Replaces the _attn_fwd launch
- * (FA:1036-1057; kernel FA:91-315).
+ * (FA:1036-1057; kernel FA:91-315).  o_res: NULL, or a buffer of
+ * farope_attn_residual_elems(desc) elements (filled when that is > 0).
  */
 int farope_attn_fwd(const farope_attn_desc* desc,
                     const void* q, const int64_t q_stride[4],
                     const void* k, const int64_t k_stride[4],
                     const void* v, const int64_t v_stride[4],
                     const float* rope_packed,
-                    void* o, const int64_t o_stride[4],
+                    void* o, const int64_t o_stride[4], void* o_res,
                     float* lse, void* stream);
 
-/* delta = rowsum(dout * o) in fp32.  Replaces _attn_bwd_preprocess
- * (launch FA:1076-1082; kernel FA:325-357). */
+/* delta = rowsum(dout * (o + o_res)) in fp32 (o_res may be NULL).  Replaces
+ * _attn_bwd_preprocess (launch FA:1076-1082; kernel FA:325-357). */
 int farope_attn_bwd_preprocess(const farope_attn_desc* desc,
-                               const void* o, const int64_t o_stride[4],
+                               const void* o, const int64_t o_stride[4], const void* o_res,
                                const void* dout, const int64_t dout_stride[4],
                                float* delta, void* stream);
 
@@ -131,12 +144,13 @@ int farope_attn_bwd_dq(const farope_attn_desc* desc,
  * picks the fused one-launch kernel when the plane fits on chip (D = 64,
  * N <= 256), else dq (which also writes delta) followed by dk/dv.
  * delta_ws: caller-owned fp32 workspace of batch*heads*seq_len elements.
+ * o_res: NULL, or the residual buffer the forward filled.
  */
 int farope_attn_bwd(const farope_attn_desc* desc,
                     const void* q, const int64_t q_stride[4],
                     const void* k, const int64_t k_stride[4],
                     const void* v, const int64_t v_stride[4],
-                    const void* o, const int64_t o_stride[4],
+                    const void* o, const int64_t o_stride[4], const void* o_res,
                     const void* dout, const int64_t dout_stride[4],
                     const float* lse, const float* rope_packed,
                     void* dq, const int64_t dq_stride[4],
@@ -160,7 +174,7 @@ int farope_attn_bwd_noalloc(const farope_attn_desc* desc,
                             const void* q, const int64_t q_stride[4],
                             const void* k, const int64_t k_stride[4],
                             const void* v, const int64_t v_stride[4],
-                            const void* o, const int64_t o_stride[4],
+                            const void* o, const int64_t o_stride[4], const void* o_res,
                             const void* dout, const int64_t dout_stride[4],
                             const float* lse, const float* rope_packed,
                             void* dq, const int64_t dq_stride[4],

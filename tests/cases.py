@@ -61,18 +61,14 @@ def rounding_floor(ref: torch.Tensor, dtype):
 FLOOR_MULT = 2.0
 
 # Committed per-case ceilings (max_abs_err, mean_abs_err) where the error of
-# the standard algorithm itself exceeds FLOOR_MULT x the storage floor.  The
-# excess is delta = rowsum(dO * O) taken from the bf16-stored O (FA:352-354
-# does the same; so does every implementation that returns O in bf16): with
-# an exact delta the same kernel arithmetic gives dQ / dK at 1.6x the floor
-# (fp64 model of the kernel's rounding on these inputs).  Each ceiling is
+# the standard algorithm itself exceeds FLOOR_MULT x the storage floor, each
 # about 1.15x the error measured on MI355X, so a regression shows.
-#   hires  (B32 H12 N1025 D128, inputs x2): measured dQ 1.52e-1 / 2.62e-3,
-#          dK 1.27e-1 / 2.27e-3 (floors 6.2e-2 / 1.12e-3 and 6.0e-2 / 1.08e-3)
-#   N = 2  (side 1 + CLS, D64): measured dQ 1.26e-2 / 1.09e-3, dK 1.29e-2 / 1.13e-3
+#   N = 2  (side 1 + CLS, D64): measured dQ 1.26e-2 / 1.13e-3, dK 1.44e-2 / 1.13e-3
+#          against floors of 2.5e-4 / 3.0e-4 (two tokens: delta = rowsum(dO * O)
+#          from the bf16-stored O dominates, FA:352-354 does the same; head_dim 64
+#          keeps plain bf16 operands and no O residual)
 CEILINGS = {
-    "hires": {"dQ": (1.75e-1, 3.0e-3), "dK": (1.45e-1, 2.6e-3)},
-    "side1-cls1-D64": {"dQ": (3e-2, 1.25e-3), "dK": (3e-2, 1.3e-3)},
+    "side1-cls1-D64": {"dQ": (3e-2, 1.3e-3), "dK": (3e-2, 1.3e-3)},
 }
 
 

@@ -97,10 +97,15 @@ def test_fake_kernels_shapes_and_dtypes():
     with FakeTensorMode():
         q = torch.empty(2, 3, 197, 64, dtype=torch.bfloat16, device="cuda")
         rope = torch.empty(197 * 32 * 2, dtype=torch.float32, device="cuda")
-        o, lse = torch.ops.farope.attn_fwd(q, q, q, rope, 196, True, 0.125, 2)
+        o, lse, res = torch.ops.farope.attn_fwd(q, q, q, rope, 196, True, 0.125, 2)
         assert o.shape == q.shape and o.dtype == q.dtype
         assert lse.shape == (2, 3, 197) and lse.dtype == torch.float32
-        dq, dk, dv = torch.ops.farope.attn_bwd(q, q, q, q, o, lse, rope, 196, True, 0.125, 2)
+        assert res.shape == (0,)   # head_dim 64: no residual
+        q128 = torch.empty(2, 3, 197, 128, dtype=torch.bfloat16, device="cuda")
+        rope128 = torch.empty(197 * 64 * 2, dtype=torch.float32, device="cuda")
+        o2, _, res2 = torch.ops.farope.attn_fwd(q128, q128, q128, rope128, 196, True, 0.088, 2)
+        assert res2.shape == q128.shape and res2.dtype == torch.bfloat16
+        dq, dk, dv = torch.ops.farope.attn_bwd(q, q, q, q, o, lse, rope, 196, True, 0.125, 2, res)
         for t in (dq, dk, dv):
             assert t.shape == q.shape and t.dtype == q.dtype
         cosp = torch.empty(196, 32, dtype=torch.float32, device="cuda")
@@ -210,3 +215,18 @@ def test_packed_table_cache_invalidation(monkeypatch):
     n = len(calls)
     clone.packed()
     assert len(calls) == n + 1
+
+
+def test_residual_rule_matches_library():
+    """attention._uses_residual (used for allocation and the fake kernels)
+    agrees with the library's farope_attn_residual_elems for every dtype pair
+    and head_dim."""
+    from triton_fused_rope_flash_attn_amd import _lib
+
+    for io in (_lib.F32, _lib.F16, _lib.BF16):
+        for ct in (_lib.F32, _lib.F16, _lib.BF16):
+            for D in (32, 64, 128, 256):
+                desc = _lib.make_desc(2, 3, 197, D, 196, True, io, ct, D ** -0.5)
+                n = _lib.residual_elems(desc)
+                assert (n > 0) == attention._uses_residual(io, ct, D), (io, ct, D)
+                assert n in (0, 2 * 3 * 197 * D)

@@ -71,6 +71,6 @@ def test_gpu_path_matches_fixture(has_cls, dtype, tol):
         print(f"[golden {t} {dtype}] {name}: max_abs_err={err:.3e}", flush=True)
         assert err < tol * max(1.0, float(np.abs(want).max())), name
     # LSE through the raw op
-    o2, lse = torch.ops.farope.attn_fwd(q.detach(), k.detach(), v.detach(), table.packed(), 4, has_cls,
+    o2, lse, _ = torch.ops.farope.attn_fwd(q.detach(), k.detach(), v.detach(), table.packed(), 4, has_cls,
                                          1 / math.sqrt(64), {torch.float32: 0, torch.bfloat16: 2}[dtype])
     assert np.abs(lse.cpu().numpy() - g[f"{t}_lse"]).max() < tol * 10

@@ -114,7 +114,7 @@ def test_lse_matches_logsumexp():
     q, k, v, _ = make_inputs(cfg, DEV)
     table = CosSinTable(ROPE_BASE, cfg["side"], cfg["D"], device=DEV)
     N, D = seq_len(cfg), cfg["D"]
-    o, lse = torch.ops.farope.attn_fwd(q, k, v, table.packed(), N - 1, True, 1 / math.sqrt(D), _lib.BF16)
+    o, lse, _ = torch.ops.farope.attn_fwd(q, k, v, table.packed(), N - 1, True, 1 / math.sqrt(D), _lib.BF16)
     ref = torch_ref.logsumexp_rows(q.float(), k.float(), table.COSP, table.SINP, True)
     mx, _ = errors(lse, ref)
     _say(f"[lse] max_abs_err={mx:.3e}")
@@ -284,8 +284,8 @@ def test_split_entry_points_match_fused():
     B, H, N, D = q.shape
     rope = table.packed()
     scale = 1 / math.sqrt(D)
-    o, lse = torch.ops.farope.attn_fwd(q, k, v, rope, N - 1, True, scale, _lib.BF16)
-    dq, dk, dv = torch.ops.farope.attn_bwd(do, q, k, v, o, lse, rope, N - 1, True, scale, _lib.BF16)
+    o, lse, res = torch.ops.farope.attn_fwd(q, k, v, rope, N - 1, True, scale, _lib.BF16)
+    dq, dk, dv = torch.ops.farope.attn_bwd(do, q, k, v, o, lse, rope, N - 1, True, scale, _lib.BF16, res)
     desc = _lib.make_desc(B, H, N, D, N - 1, True, _lib.BF16, _lib.BF16, scale)
     delta = torch.empty(B, H, N, device=DEV, dtype=torch.float32)
     dq2, dk2, dv2 = (torch.empty_like(q) for _ in range(3))

@@ -87,7 +87,7 @@ def _call_fwd(lib, desc, q=16, lse=16, rope=16):
     s = _lib.Stride4(0, 0, 0, 1)
     return lib.farope_attn_fwd(
         ctypes.byref(desc) if desc is not None else None,
-        q, s, 16, s, 16, s, rope, 16, s, lse, None,
+        q, s, 16, s, 16, s, rope, 16, s, None, lse, None,
     )
 
 
@@ -121,10 +121,11 @@ def test_fwd_rejects_null_and_misaligned(lib):
 def test_bwd_entry_points_reject_bad_arguments(lib):
     s = _lib.Stride4(0, 0, 0, 1)
     bad = _lib.make_desc(2, 3, 197, 60, 196, True, _lib.BF16, _lib.BF16, 0.125)
-    assert lib.farope_attn_bwd(ctypes.byref(bad), *([16, s] * 5), 16, 16, *([16, s] * 3), 16, None) == _lib.ERR_HEAD_DIM
+    assert lib.farope_attn_bwd(ctypes.byref(bad), *([16, s] * 4), None, 16, s, 16, 16, *([16, s] * 3), 16, None) == _lib.ERR_HEAD_DIM
     good = _lib.make_desc(2, 3, 197, 64, 196, True, _lib.BF16, _lib.BF16, 0.125)
-    assert lib.farope_attn_bwd(ctypes.byref(good), *([16, s] * 5), None, 16, *([16, s] * 3), 16, None) == _lib.ERR_NULL
-    assert lib.farope_attn_bwd_preprocess(ctypes.byref(bad), 16, s, 16, s, 16, None) == _lib.ERR_HEAD_DIM
+    assert lib.farope_attn_bwd(ctypes.byref(good), *([16, s] * 4), None, 16, s, None, 16, *([16, s] * 3), 16, None) == _lib.ERR_NULL
+    assert lib.farope_attn_bwd(ctypes.byref(good), *([16, s] * 4), 24, 16, s, 16, 16, *([16, s] * 3), 16, None) == _lib.ERR_ALIGN
+    assert lib.farope_attn_bwd_preprocess(ctypes.byref(bad), 16, s, None, 16, s, 16, None) == _lib.ERR_HEAD_DIM
     assert lib.farope_attn_bwd_dq(ctypes.byref(good), *([16, s] * 4), 16, 3, 16, 16, s, None) == _lib.ERR_ALIGN
     assert lib.farope_attn_bwd_dk_dv(ctypes.byref(good), *([16, s] * 4), 16, 16, 16, 16, s, None, s, None) == _lib.ERR_NULL
     assert lib.farope_rope_pack(16, 32, 1, 16, 32, 1, 196, 31, 16, None) == _lib.ERR_TABLE
@@ -140,7 +141,7 @@ def test_noalloc_bwd_rejects_oversize_before_any_launch(lib):
     N = 1025   # split path; 4096 planes x 1025 rows > 4 Mi rows
     big = _lib.make_desc(64, 64, N, 128, N - 1, True, _lib.BF16, _lib.BF16, 128 ** -0.5)
     assert 64 * 64 * N > _lib.NOALLOC_MAX_ROWS
-    assert lib.farope_attn_bwd_noalloc(ctypes.byref(big), *([16, s] * 5), 16, 16, *([16, s] * 3), None) == _lib.ERR_SCRATCH
+    assert lib.farope_attn_bwd_noalloc(ctypes.byref(big), *([16, s] * 4), None, 16, s, 16, 16, *([16, s] * 3), None) == _lib.ERR_SCRATCH
     bad = _lib.make_desc(2, 3, 197, 60, 196, True, _lib.BF16, _lib.BF16, 0.125)
-    assert lib.farope_attn_bwd_noalloc(ctypes.byref(bad), *([16, s] * 5), 16, 16, *([16, s] * 3), None) == _lib.ERR_HEAD_DIM
+    assert lib.farope_attn_bwd_noalloc(ctypes.byref(bad), *([16, s] * 4), None, 16, s, 16, 16, *([16, s] * 3), None) == _lib.ERR_HEAD_DIM
     assert "static workspace" in _lib.strerror(_lib.ERR_SCRATCH)

@@ -32,13 +32,13 @@ def _one(B, H, side, has_cls, D, seed):
     rope = table.packed()
     scale = 1.0 / math.sqrt(D)
     n_pos = side * side
-    o, lse = torch.ops.farope.attn_fwd(q, k, v, rope, n_pos, has_cls, scale, _lib.BF16)
+    o, lse, res = torch.ops.farope.attn_fwd(q, k, v, rope, n_pos, has_cls, scale, _lib.BF16)
     desc = _lib.make_desc(B, H, N, D, n_pos, has_cls, _lib.BF16, _lib.BF16, scale)
     ref = [torch.empty_like(q) for _ in range(3)]
     delta = torch.empty(B, H, N, device=DEV, dtype=torch.float32)
-    _lib.attn_bwd(desc, q, k, v, o, do, lse, rope, *ref, delta)
+    _lib.attn_bwd(desc, q, k, v, o, do, lse, rope, *ref, delta, res)
     got = [torch.full_like(q, float("nan")) for _ in range(3)]
-    _lib.attn_bwd_noalloc(desc, q, k, v, o, do, lse, rope, *got)
+    _lib.attn_bwd_noalloc(desc, q, k, v, o, do, lse, rope, *got, res)
     torch.cuda.synchronize()
     for name, a, b in zip(("dQ", "dK", "dV"), got, ref):
         assert torch.isfinite(a).all(), name

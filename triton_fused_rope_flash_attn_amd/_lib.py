@@ -30,6 +30,7 @@ EXPORTS = (
     "farope_strerror",
     "farope_rope_packed_elems",
     "farope_rope_pack",
+    "farope_attn_residual_elems",
     "farope_attn_fwd",
     "farope_attn_bwd_preprocess",
     "farope_attn_bwd_dk_dv",
@@ -66,8 +67,9 @@ _SIGNATURES = {
     "farope_strerror": (ctypes.c_char_p, [ctypes.c_int]),
     "farope_rope_packed_elems": (ctypes.c_size_t, [_I32, _I32]),
     "farope_rope_pack": (ctypes.c_int, [_P, _I64, _I64, _P, _I64, _I64, _I32, _I32, _P, _P]),
-    "farope_attn_fwd": (ctypes.c_int, [_D, _P, _S, _P, _S, _P, _S, _P, _P, _S, _P, _P]),
-    "farope_attn_bwd_preprocess": (ctypes.c_int, [_D, _P, _S, _P, _S, _P, _P]),
+    "farope_attn_residual_elems": (ctypes.c_size_t, [_D]),
+    "farope_attn_fwd": (ctypes.c_int, [_D, _P, _S, _P, _S, _P, _S, _P, _P, _S, _P, _P, _P]),
+    "farope_attn_bwd_preprocess": (ctypes.c_int, [_D, _P, _S, _P, _P, _S, _P, _P]),
     "farope_attn_bwd_dk_dv": (
         ctypes.c_int,
         [_D, _P, _S, _P, _S, _P, _S, _P, _S, _P, _P, _P, _P, _S, _P, _S, _P],
@@ -75,11 +77,11 @@ _SIGNATURES = {
     "farope_attn_bwd_dq": (ctypes.c_int, [_D, _P, _S, _P, _S, _P, _S, _P, _S, _P, _P, _P, _P, _S, _P]),
     "farope_attn_bwd": (
         ctypes.c_int,
-        [_D, _P, _S, _P, _S, _P, _S, _P, _S, _P, _S, _P, _P, _P, _S, _P, _S, _P, _S, _P, _P],
+        [_D, _P, _S, _P, _S, _P, _S, _P, _S, _P, _P, _S, _P, _P, _P, _S, _P, _S, _P, _S, _P, _P],
     ),
     "farope_attn_bwd_noalloc": (
         ctypes.c_int,
-        [_D, _P, _S, _P, _S, _P, _S, _P, _S, _P, _S, _P, _P, _P, _S, _P, _S, _P, _S, _P],
+        [_D, _P, _S, _P, _S, _P, _S, _P, _S, _P, _P, _S, _P, _P, _P, _S, _P, _S, _P, _S, _P],
     ),
     "farope_tile_config": (ctypes.c_int, [_D, _I32, ctypes.POINTER(ctypes.c_int32)]),
 }
@@ -147,20 +149,30 @@ def rope_pack(cosp: torch.Tensor, sinp: torch.Tensor, out: torch.Tensor) -> None
     check(rc, "farope_rope_pack")
 
 
-def attn_fwd(desc: AttnDesc, q, k, v, rope, o, lse) -> None:
+def residual_elems(desc: AttnDesc) -> int:
+    """Elements of the O-residual buffer the call uses (0: none); see farope_attn_residual_elems."""
+    return int(load().farope_attn_residual_elems(ctypes.byref(desc)))
+
+
+def _ptr(t) -> int | None:
+    """Device pointer of an optional buffer: None for a missing or empty tensor."""
+    return t.data_ptr() if t is not None and t.numel() > 0 else None
+
+
+def attn_fwd(desc: AttnDesc, q, k, v, rope, o, lse, o_res=None) -> None:
     rc = load().farope_attn_fwd(
         ctypes.byref(desc),
         q.data_ptr(), strides(q), k.data_ptr(), strides(k), v.data_ptr(), strides(v),
-        rope.data_ptr(), o.data_ptr(), strides(o), lse.data_ptr(), stream_of(q),
+        rope.data_ptr(), o.data_ptr(), strides(o), _ptr(o_res), lse.data_ptr(), stream_of(q),
     )
     check(rc, "farope_attn_fwd")
 
 
-def attn_bwd(desc: AttnDesc, q, k, v, o, do, lse, rope, dq, dk, dv, delta) -> None:
+def attn_bwd(desc: AttnDesc, q, k, v, o, do, lse, rope, dq, dk, dv, delta, o_res=None) -> None:
     rc = load().farope_attn_bwd(
         ctypes.byref(desc),
         q.data_ptr(), strides(q), k.data_ptr(), strides(k), v.data_ptr(), strides(v),
-        o.data_ptr(), strides(o), do.data_ptr(), strides(do),
+        o.data_ptr(), strides(o), _ptr(o_res), do.data_ptr(), strides(do),
         lse.data_ptr(), rope.data_ptr(),
         dq.data_ptr(), strides(dq), dk.data_ptr(), strides(dk), dv.data_ptr(), strides(dv),
         delta.data_ptr(), stream_of(q),
@@ -168,12 +180,12 @@ def attn_bwd(desc: AttnDesc, q, k, v, o, do, lse, rope, dq, dk, dv, delta) -> No
     check(rc, "farope_attn_bwd")
 
 
-def attn_bwd_noalloc(desc: AttnDesc, q, k, v, o, do, lse, rope, dq, dk, dv) -> None:
+def attn_bwd_noalloc(desc: AttnDesc, q, k, v, o, do, lse, rope, dq, dk, dv, o_res=None) -> None:
     """farope_attn_bwd_noalloc: the backward with the library's static delta workspace."""
     rc = load().farope_attn_bwd_noalloc(
         ctypes.byref(desc),
         q.data_ptr(), strides(q), k.data_ptr(), strides(k), v.data_ptr(), strides(v),
-        o.data_ptr(), strides(o), do.data_ptr(), strides(do),
+        o.data_ptr(), strides(o), _ptr(o_res), do.data_ptr(), strides(do),
         lse.data_ptr(), rope.data_ptr(),
         dq.data_ptr(), strides(dq), dk.data_ptr(), strides(dk), dv.data_ptr(), strides(dv),
         stream_of(q),
@@ -181,9 +193,9 @@ def attn_bwd_noalloc(desc: AttnDesc, q, k, v, o, do, lse, rope, dq, dk, dv) -> N
     check(rc, "farope_attn_bwd_noalloc")
 
 
-def attn_bwd_preprocess(desc: AttnDesc, o, do, delta) -> None:
+def attn_bwd_preprocess(desc: AttnDesc, o, do, delta, o_res=None) -> None:
     rc = load().farope_attn_bwd_preprocess(
-        ctypes.byref(desc), o.data_ptr(), strides(o), do.data_ptr(), strides(do),
+        ctypes.byref(desc), o.data_ptr(), strides(o), _ptr(o_res), do.data_ptr(), strides(do),
         delta.data_ptr(), stream_of(o),
     )
     check(rc, "farope_attn_bwd_preprocess")

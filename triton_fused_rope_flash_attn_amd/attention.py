@@ -72,6 +72,13 @@ def _check_rope(rope: torch.Tensor, n_pos: int, d: int, device) -> None:
         raise RuntimeError(f"farope: RoPE table on {rope.device}, tensors on {device}")
 
 
+def _uses_residual(io_dtype: int, compute_dtype: int, head_dim: int) -> bool:
+    """Whether the call keeps O's rounding residual for the backward's delta:
+    bf16 tensors computed in bf16 at head_dim >= 128 (the rule of
+    farope_attn_residual_elems, which the CPU tests check this against)."""
+    return io_dtype == _lib.BF16 and compute_dtype == _lib.BF16 and head_dim >= 128
+
+
 # ---------------------------------------------------------------------------
 # custom ops
 # ---------------------------------------------------------------------------
@@ -85,25 +92,31 @@ def attn_fwd(
     has_cls: bool,
     softmax_scale: float,
     compute_dtype: int,
-) -> tuple[torch.Tensor, torch.Tensor]:
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """-> (O, LSE, O_res).  O_res is O's rounding residual bf16(O - bf16(O))
+    [B, H, N, D] where the call keeps one (see _uses_residual), else empty."""
     _check_qkv(q, k, v)
     B, H, N, D = q.shape
     _check_rope(rope, n_pos, D, q.device)
     o = torch.empty((B, H, N, D), dtype=q.dtype, device=q.device)
     lse = torch.empty((B, H, N), dtype=torch.float32, device=q.device)
-    desc = _lib.make_desc(B, H, N, D, n_pos, has_cls, _lib.DTYPE_CODE[q.dtype], compute_dtype,
-                          softmax_scale)
+    io = _lib.DTYPE_CODE[q.dtype]
+    res = _uses_residual(io, compute_dtype, D)
+    o_res = torch.empty((B, H, N, D) if res else (0,), dtype=q.dtype, device=q.device)
+    desc = _lib.make_desc(B, H, N, D, n_pos, has_cls, io, compute_dtype, softmax_scale)
     with torch.cuda.device(q.device):
-        _lib.attn_fwd(desc, q, k, v, rope, o, lse)
-    return o, lse
+        _lib.attn_fwd(desc, q, k, v, rope, o, lse, o_res)
+    return o, lse, o_res
 
 
 @attn_fwd.register_fake
 def _attn_fwd_fake(q, k, v, rope, n_pos, has_cls, softmax_scale, compute_dtype):
     B, H, N, D = q.shape
+    res = _uses_residual(_lib.DTYPE_CODE.get(q.dtype, -1), compute_dtype, D)
     return (
         q.new_empty((B, H, N, D)),
         q.new_empty((B, H, N), dtype=torch.float32),
+        q.new_empty((B, H, N, D) if res else (0,)),
     )
 
 
@@ -120,7 +133,9 @@ def attn_bwd(
     has_cls: bool,
     softmax_scale: float,
     compute_dtype: int,
+    o_res: torch.Tensor,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """-> (dQ, dK, dV).  o_res: attn_fwd's third output (may be empty)."""
     _check_qkv(q, k, v)
     B, H, N, D = q.shape
     _check_rope(rope, n_pos, D, q.device)
@@ -136,37 +151,39 @@ def attn_bwd(
     delta = torch.empty((B, H, N), dtype=torch.float32, device=q.device)
     desc = _lib.make_desc(B, H, N, D, n_pos, has_cls, _lib.DTYPE_CODE[q.dtype], compute_dtype,
                           softmax_scale)
+    if o_res.numel() and (o_res.shape != q.shape or o_res.dtype != q.dtype or not o_res.is_contiguous()):
+        raise ValueError("farope: O_res must be contiguous with Q's shape and dtype, or empty")
     with torch.cuda.device(q.device):
-        _lib.attn_bwd(desc, q, k, v, o, do, lse, rope, dq, dk, dv, delta)
+        _lib.attn_bwd(desc, q, k, v, o, do, lse, rope, dq, dk, dv, delta, o_res)
     return dq, dk, dv
 
 
 @attn_bwd.register_fake
-def _attn_bwd_fake(do, q, k, v, o, lse, rope, n_pos, has_cls, softmax_scale, compute_dtype):
+def _attn_bwd_fake(do, q, k, v, o, lse, rope, n_pos, has_cls, softmax_scale, compute_dtype, o_res):
     B, H, N, D = q.shape
     return q.new_empty((B, H, N, D)), k.new_empty((B, H, N, D)), v.new_empty((B, H, N, D))
 
 
 def _fwd_setup_context(ctx, inputs, output):
     q, k, v, rope, n_pos, has_cls, softmax_scale, compute_dtype = inputs
-    o, lse = output
-    ctx.mark_non_differentiable(lse)
+    o, lse, o_res = output
+    ctx.mark_non_differentiable(lse, o_res)
     # LSE's incoming gradient is never used: without this, autograd fills a
     # zero tensor for it on every backward (an extra kernel per step)
     ctx.set_materialize_grads(False)
-    ctx.save_for_backward(q, k, v, o, lse, rope)
+    ctx.save_for_backward(q, k, v, o, lse, rope, o_res)
     ctx.n_pos = n_pos
     ctx.has_cls = has_cls
     ctx.softmax_scale = softmax_scale
     ctx.compute_dtype = compute_dtype
 
 
-def _fwd_backward(ctx, do, _dlse):
+def _fwd_backward(ctx, do, _dlse, _dres):
     if do is None:   # O received no gradient (grads are not materialised)
         return None, None, None, None, None, None, None, None
-    q, k, v, o, lse, rope = ctx.saved_tensors
+    q, k, v, o, lse, rope, o_res = ctx.saved_tensors
     dq, dk, dv = attn_bwd(do, q, k, v, o, lse, rope, ctx.n_pos, ctx.has_cls,
-                          ctx.softmax_scale, ctx.compute_dtype)
+                          ctx.softmax_scale, ctx.compute_dtype, o_res)
     return dq, dk, dv, None, None, None, None, None
 
 
@@ -220,25 +237,26 @@ class TritonAttention(torch.autograd.Function):
 
     ``forward(ctx, Q, K, V, cos_sin, H_img=14, has_cls=True)`` -> O;
     ``backward`` returns gradients for Q, K, V only.  Saved for backward:
-    Q, K, V, O, LSE and the packed table (the reference saves COSP/SINP).
+    Q, K, V, O, LSE, the packed table (the reference saves COSP/SINP) and
+    O's rounding residual where the call keeps one.
     """
 
     @staticmethod
     def forward(ctx, Q, K, V, cos_sin, H_img=14, has_cls=True):
         rope, n_pos, has_cls, scale, comp = _prepare(Q, K, V, cos_sin, H_img, has_cls)
-        O, M = attn_fwd(Q, K, V, rope, n_pos, has_cls, scale, comp)
+        O, M, R = attn_fwd(Q, K, V, rope, n_pos, has_cls, scale, comp)
         ctx.softmax_scale = scale
         ctx.comp = comp
         ctx.has_cls = has_cls
         ctx.n_pos = n_pos
-        ctx.save_for_backward(Q, K, V, O, M, rope)
+        ctx.save_for_backward(Q, K, V, O, M, rope, R)
         return O
 
     @staticmethod
     def backward(ctx, dO):
-        Q, K, V, O, M, rope = ctx.saved_tensors
+        Q, K, V, O, M, rope, R = ctx.saved_tensors
         dQ, dK, dV = attn_bwd(dO, Q, K, V, O, M, rope, ctx.n_pos, ctx.has_cls,
-                              ctx.softmax_scale, ctx.comp)
+                              ctx.softmax_scale, ctx.comp, R)
         return dQ, dK, dV, None, None, None
 
 
@@ -265,5 +283,5 @@ def sdpa_triton_fa_rope(
         if H_img * H_img != n_pos:
             raise ValueError(f"RoPE table has {n_pos} rows, not a square H_img x H_img grid")
     rope, n_pos, has_cls, scale, comp = _prepare(Q, K, V, cos_sin, H_img, has_cls)
-    O, _ = attn_fwd(Q, K, V, rope, n_pos, has_cls, scale, comp)
+    O, _, _ = attn_fwd(Q, K, V, rope, n_pos, has_cls, scale, comp)
     return O

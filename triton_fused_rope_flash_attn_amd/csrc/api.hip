@@ -151,7 +151,7 @@ int scratch_ptr(float** out) {
 
 int bwd_impl(const farope_attn_desc* desc, const void* q, const int64_t q_stride[4],
              const void* k, const int64_t k_stride[4], const void* v, const int64_t v_stride[4],
-             const void* o, const int64_t o_stride[4], const void* dout,
+             const void* o, const int64_t o_stride[4], const void* o_res, const void* dout,
              const int64_t dout_stride[4], const float* lse, const float* rope_packed, void* dq,
              const int64_t dq_stride[4], void* dk, const int64_t dk_stride[4], void* dv,
              const int64_t dv_stride[4], float* delta_ws, bool static_ws, void* stream) {
@@ -178,9 +178,11 @@ int bwd_impl(const farope_attn_desc* desc, const void* q, const int64_t q_stride
   } else if (!fused) {
     FAROPE_TRY(check_ptr(delta_ws, 4));
   }
+  if (o_res) FAROPE_TRY(check_ptr(o_res, 16));
   BwdParams p = {};
   fill_common(p, desc, rope_packed);
   p.q = q; p.k = k; p.v = v; p.o = o; p.dout = dout;
+  p.o_res = o_residual(desc->io_dtype, desc->compute_dtype, desc->head_dim) ? o_res : nullptr;
   p.dq = dq; p.dk = dk; p.dv = dv;
   p.lse = lse; p.delta = delta_ws;
   copy4(p.sq, q_stride); copy4(p.sk, k_stride); copy4(p.sv, v_stride); copy4(p.so, o_stride);
@@ -267,10 +269,16 @@ int farope_tile_config(const farope_attn_desc* desc, int32_t which, int32_t out[
   return FAROPE_OK;
 }
 
+size_t farope_attn_residual_elems(const farope_attn_desc* desc) {
+  if (check_desc(desc) != FAROPE_OK) return 0;
+  if (!o_residual(desc->io_dtype, desc->compute_dtype, desc->head_dim)) return 0;
+  return (size_t)desc->batch * desc->heads * desc->seq_len * desc->head_dim;
+}
+
 int farope_attn_fwd(const farope_attn_desc* desc, const void* q, const int64_t q_stride[4],
                     const void* k, const int64_t k_stride[4], const void* v,
                     const int64_t v_stride[4], const float* rope_packed, void* o,
-                    const int64_t o_stride[4], float* lse, void* stream) {
+                    const int64_t o_stride[4], void* o_res, float* lse, void* stream) {
   FAROPE_TRY(check_desc(desc));
   if (!q_stride || !k_stride || !v_stride || !o_stride) return FAROPE_ERR_NULL;
   const int es = elem_size(desc->io_dtype);
@@ -280,9 +288,11 @@ int farope_attn_fwd(const farope_attn_desc* desc, const void* q, const int64_t q
   FAROPE_TRY(check_ptr(o, es));
   FAROPE_TRY(check_ptr(lse, 4));
   FAROPE_TRY(check_ptr(rope_packed, 16));
+  if (o_res) FAROPE_TRY(check_ptr(o_res, 16));
 
   FwdParams p;
   p.q = q; p.k = k; p.v = v; p.o = o; p.lse = lse;
+  p.o_res = o_residual(desc->io_dtype, desc->compute_dtype, desc->head_dim) ? o_res : nullptr;
   copy4(p.sq, q_stride); copy4(p.sk, k_stride); copy4(p.sv, v_stride); copy4(p.so, o_stride);
   p.rope = rope_packed;
   p.B = desc->batch; p.H = desc->heads; p.N = desc->seq_len; p.has_cls = desc->has_cls;
@@ -298,7 +308,7 @@ int farope_attn_fwd(const farope_attn_desc* desc, const void* q, const int64_t q
 }
 
 int farope_attn_bwd_preprocess(const farope_attn_desc* desc, const void* o,
-                               const int64_t o_stride[4], const void* dout,
+                               const int64_t o_stride[4], const void* o_res, const void* dout,
                                const int64_t dout_stride[4], float* delta, void* stream) {
   FAROPE_TRY(check_desc(desc));
   if (!o_stride || !dout_stride) return FAROPE_ERR_NULL;
@@ -309,6 +319,8 @@ int farope_attn_bwd_preprocess(const farope_attn_desc* desc, const void* o,
   BwdParams p = {};
   fill_common(p, desc, nullptr);
   p.o = o; p.dout = dout; p.delta = delta;
+  if (o_res) FAROPE_TRY(check_ptr(o_res, 16));
+  p.o_res = o_residual(desc->io_dtype, desc->compute_dtype, desc->head_dim) ? o_res : nullptr;
   copy4(p.so, o_stride); copy4(p.sdo, dout_stride);
   p.vec_o = vec_ok(o, o_stride, es, desc->seq_len, desc->head_dim);
   p.vec_do = vec_ok(dout, dout_stride, es, desc->seq_len, desc->head_dim);
@@ -387,24 +399,24 @@ int farope_attn_bwd_dq(const farope_attn_desc* desc, const void* q, const int64_
 int farope_attn_bwd(const farope_attn_desc* desc, const void* q, const int64_t q_stride[4],
                     const void* k, const int64_t k_stride[4], const void* v,
                     const int64_t v_stride[4], const void* o, const int64_t o_stride[4],
-                    const void* dout, const int64_t dout_stride[4], const float* lse,
+                    const void* o_res, const void* dout, const int64_t dout_stride[4], const float* lse,
                     const float* rope_packed, void* dq, const int64_t dq_stride[4], void* dk,
                     const int64_t dk_stride[4], void* dv, const int64_t dv_stride[4],
                     float* delta_ws, void* stream) {
-  return bwd_impl(desc, q, q_stride, k, k_stride, v, v_stride, o, o_stride, dout, dout_stride, lse,
-                  rope_packed, dq, dq_stride, dk, dk_stride, dv, dv_stride, delta_ws, false, stream);
+  return bwd_impl(desc, q, q_stride, k, k_stride, v, v_stride, o, o_stride, o_res, dout, dout_stride,
+                  lse, rope_packed, dq, dq_stride, dk, dk_stride, dv, dv_stride, delta_ws, false, stream);
 }
 
 int farope_attn_bwd_noalloc(const farope_attn_desc* desc, const void* q,
                             const int64_t q_stride[4], const void* k, const int64_t k_stride[4],
                             const void* v, const int64_t v_stride[4], const void* o,
-                            const int64_t o_stride[4], const void* dout,
+                            const int64_t o_stride[4], const void* o_res, const void* dout,
                             const int64_t dout_stride[4], const float* lse,
                             const float* rope_packed, void* dq, const int64_t dq_stride[4],
                             void* dk, const int64_t dk_stride[4], void* dv,
                             const int64_t dv_stride[4], void* stream) {
-  return bwd_impl(desc, q, q_stride, k, k_stride, v, v_stride, o, o_stride, dout, dout_stride, lse,
-                  rope_packed, dq, dq_stride, dk, dk_stride, dv, dv_stride, nullptr, true, stream);
+  return bwd_impl(desc, q, q_stride, k, k_stride, v, v_stride, o, o_stride, o_res, dout, dout_stride,
+                  lse, rope_packed, dq, dq_stride, dk, dk_stride, dv, dv_stride, nullptr, true, stream);
 }
 
 }  // extern "C"

@@ -53,6 +53,12 @@ __global__ void __launch_bounds__(256) bwd_pre_kernel(const BwdParams p) {
     load8(G + 8 * cc * p.sdo[3], p.sdo[3], p.vec_do, g);
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc += o[e] * g[e];
+    if (p.o_res) {   // O's rounding residual (contiguous [B, H, N, D])
+      float r[8];
+      load8(static_cast<const IO*>(p.o_res) + grow * D + 8 * cc, 1, true, r);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc += r[e] * g[e];
+    }
   }
 #pragma unroll
   for (int m = 1; m < CPR; m <<= 1) acc += __shfl_xor(acc, m);
@@ -134,6 +140,11 @@ bwd_dq_kernel(const BwdParams p) {
           load8(O + row * p.so[2] + c0 * p.so[3], p.so[3], p.vec_o, o);
 #pragma unroll
           for (int e = 0; e < 8; ++e) dsum += g[e] * o[e];
+          if (p.o_res) {   // O's rounding residual (contiguous [B, H, N, D])
+            load8(static_cast<const IO*>(p.o_res) + (prow + row) * D + c0, 1, true, o);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) dsum += g[e] * o[e];
+          }
         }
       } else {
 #pragma unroll

@@ -719,6 +719,15 @@ fwd_kernel(const FwdParams p) {
   // range, and before the first item the ranges are empty.
   constexpr bool kDefer = VEC && sizeof(IO) == 2;
   u32x2 ost[kDefer ? QT : 1][DT];
+  // RES: O's rounding residual bf16(O - bf16(O)) goes to p.o_res (contiguous
+  // [B, H, N, D]) next to O, for the backward's delta; stored only when the
+  // caller gave the buffer (a uniform test)
+  constexpr bool RES = PS && std::is_same<IO, bf16>::value;
+  u32x2 ostr[kDefer && RES ? QT : 1][DT];
+  auto res4 = [](const float (&o4)[4], const IO (&h4)[4], float (&r4)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) r4[r] = o4[r] - (float)h4[r];
+  };
   float olse[QT];
   int orow[QT];
   int oplane = -1;
@@ -729,6 +738,9 @@ fwd_kernel(const FwdParams p) {
       const auto rO = make_rsrc(plane_base(p.o, p.so, pl),
                                 have ? (unsigned)(((int64_t)(N - 1) * p.so[2] + D) * ES) : 0u);
       const auto rL = make_rsrc(p.lse + (int64_t)pl * N, have ? (unsigned)N * 4u : 0u);
+      const bool res = RES && p.o_res != nullptr;
+      const auto rR = make_rsrc(static_cast<IO*>(res ? p.o_res : p.o) + (int64_t)pl * N * D,
+                                have && res ? (unsigned)N * D * ES : 0u);
       // Lane groups lg and lg^1 trade halves so that each lane writes 8
       // consecutive channels (16 bytes) per pair of 16-channel slices
       // (d0, d1): v_permlane16_swap(a, b) gives even lane groups {a, a of
@@ -748,6 +760,17 @@ fwd_kernel(const FwdParams p) {
           }
           const int ch = 16 * (d0 + (lg & 1)) + cbase;
           __builtin_amdgcn_raw_buffer_store_b128(w, rO, (unsigned)((orow[t] * (int)p.so[2] + ch) * (int)ES), 0u, 0);
+          if constexpr (RES) {
+            u32x4 wr;
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+              const auto r = __builtin_amdgcn_permlane16_swap(ostr[t][d0][k], ostr[t][d0 + 1][k], false, false);
+              wr[k] = r[0];
+              wr[2 + k] = r[1];
+            }
+            // empty range (stores dropped) when there is no residual buffer
+            __builtin_amdgcn_raw_buffer_store_b128(wr, rR, (unsigned)((orow[t] * D + ch) * (int)ES), 0u, 0);
+          }
         }
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(olse[t]), rL,
                                               (unsigned)(lg == 0 ? orow[t] : N) * 4u, 0u, 0);
@@ -822,9 +845,19 @@ fwd_kernel(const FwdParams p) {
         for (int d = 0; d < DT; ++d) {
           typedef IO io4 __attribute__((ext_vector_type(4)));
           io4 a;
+          float o4[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) a[r] = (IO)(oacc[t][d][r] * inv);
+          for (int r = 0; r < 4; ++r) {
+            o4[r] = oacc[t][d][r] * inv;
+            a[r] = (IO)o4[r];
+          }
           __builtin_memcpy(&ost[t][d], &a, 8);
+          if constexpr (RES) {
+            io4 b;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) b[r] = (IO)(o4[r] - (float)a[r]);
+            __builtin_memcpy(&ostr[t][d], &b, 8);
+          }
         }
         olse[t] = (m_run[t] + fast_log2(l)) * kLn2;
         orow[t] = (qb * NW * QT + t * NW + wave) * 16 + lr;
@@ -850,6 +883,17 @@ fwd_kernel(const FwdParams p) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) o4[r] = oacc[t][d][r] * inv;
           buf_store4<IO>(rO, (unsigned)((row * (int)p.so[2] + 16 * d + 4 * lg) * (int)ES), 0u, o4);
+          if constexpr (RES) {
+            if (p.o_res) {
+              IO h4[4];
+              float r4[4];
+#pragma unroll
+              for (int r = 0; r < 4; ++r) h4[r] = (IO)o4[r];
+              res4(o4, h4, r4);
+              const auto rR = make_rsrc(static_cast<IO*>(p.o_res) + (int64_t)plane * N * D, (unsigned)N * D * ES);
+              buf_store4<IO>(rR, (unsigned)((row * D + 16 * d + 4 * lg) * (int)ES), 0u, r4);
+            }
+          }
         }
         const float lse = (m_run[t] + fast_log2(l)) * kLn2;
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(lse), rL, (unsigned)(lg == 0 ? row : N) * 4u, 0u, 0);
@@ -868,6 +912,17 @@ fwd_kernel(const FwdParams p) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) o4[r] = oacc[t][d][r] * inv;
             store4(O + row * p.so[2] + (16 * d + 4 * lg) * p.so[3], p.so[3], vec_o, o4);
+            if constexpr (RES) {
+              if (p.o_res) {
+                IO h4[4];
+                float r4[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) h4[r] = (IO)o4[r];
+                res4(o4, h4, r4);
+                IO* R = static_cast<IO*>(p.o_res) + ((int64_t)plane * N + row) * D + 16 * d + 4 * lg;
+                store4(R, 1, true, r4);
+              }
+            }
           }
           if (lg == 0) p.lse[(int64_t)plane * N + row] = (m_run[t] + fast_log2(l)) * kLn2;
         }

@@ -14,6 +14,7 @@ struct FwdParams {
   const void* k;
   const void* v;
   void* o;
+  void* o_res;         // optional contiguous [B, H, N, D]: bf16(O - bf16(O)) (see precise_logits)
   float* lse;          // [B*H, N] fp32, natural-log log-sum-exp of the logits
   int64_t sq[4], sk[4], sv[4], so[4];
   const float* rope;   // packed (cos, sin) table [(n_pos + 1), D/2, 2]
@@ -30,6 +31,7 @@ struct BwdParams {
   const void* k;
   const void* v;
   const void* o;
+  const void* o_res;   // optional contiguous [B, H, N, D]: O's rounding residual, added to O for delta
   const void* dout;
   void* dq;
   void* dk;
@@ -70,6 +72,11 @@ hipError_t launch_rope_pack(const float* cosp, int64_t cs0, int64_t cs1, const f
 // logits); fp16 compute keeps 3 more mantissa bits and fp32 compute splits
 // every operand anyway.
 constexpr bool precise_logits(int ct, int D) { return ct == 2 /* DT_BF16 */ && D >= 128; }
+// With split-operand logits the remaining dQ / dK error is delta = rowsum(dO * O)
+// taken from the bf16-stored O.  bf16 I/O then also stores O's rounding
+// residual bf16(O - bf16(O)) (when the caller provides the buffer), and the
+// backward takes delta from O + residual.
+constexpr bool o_residual(int io, int ct, int D) { return io == 2 && precise_logits(ct, D); }
 
 // Workgroups for a persistent kernel: min(items, CUs x resident workgroups per
 // CU), with `dyn_lds` bytes of dynamic LDS per workgroup; <= 0 on a HIP error.
