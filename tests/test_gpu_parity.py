@@ -187,6 +187,66 @@ def test_ragged_and_variant_shapes(side, has_cls, D):
     _compare(f"side{side}-cls{int(has_cls)}-D{D}", ours, ref, out_dtype=torch.bfloat16, other=other)
 
 
+@pytest.mark.parametrize(
+    "side,has_cls,D,B,H,io",
+    [(16, True, 128, 2, 3, "bf16"), (16, True, 32, 2, 3, "bf16"), (16, True, 256, 2, 3, "bf16"),
+     (16, True, 128, 2, 3, "fp16"), (16, True, 128, 1, 2, "fp32"),
+     (63, True, 128, 1, 2, "bf16"), (62, False, 128, 1, 2, "bf16")],
+)
+def test_tail_rows(side, has_cls, D, B, H, io):
+    """Rows past the last full block (N % block_rows <= 8, e.g. N = 16^2 + 1, 63^2 + 1,
+    62^2): computed by the tail kernels, not by a nearly empty block.  One tail row at
+    every head dim and I/O type; two (N = 3970) and four (N = 3844, no CLS) rows."""
+    dt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[io]
+    N = side * side + int(has_cls)
+    code = _lib.DTYPE_CODE[dt]
+    desc = _lib.make_desc(B, H, N, D, N - int(has_cls), has_cls, code, code, 1 / math.sqrt(D))
+    rows = _lib.tile_config(desc, 0)[1]   # forward block rows
+    assert N >= rows and 0 < N % rows <= 8
+    cfg = dict(B=B, H=H, side=side, has_cls=has_cls, D=D, dtype=dt, scale=1.0, dout="randn")
+    q, k, v, do = make_inputs(cfg, DEV, seed=5)
+    table = CosSinTable(ROPE_BASE, side, D, device=DEV)
+    ours = _run_ours(q, k, v, do, table, has_cls)
+    ref = _ref(q, k, v, do, table, has_cls)
+    if io == "fp32":
+        _compare(f"tail-fp32-N{N}-D{D}", ours, ref, tol_max=1e-4, tol_mean=1e-5)
+    else:
+        _compare(f"tail-{io}-N{N}-D{D}", ours, ref, out_dtype=dt)
+
+
+def test_tail_rows_generic_strides_and_split_entry_points():
+    """Tail rows through the generic (d-strided) loads, and through the reference-style
+    preprocess + dk_dv + dq entry points, which must give the one-call backward's bits."""
+    B, H, side, D = 2, 2, 16, 128
+    N = side * side + 1
+    g = torch.Generator().manual_seed(6)
+    base = [torch.randn(B, H, D, N, generator=g).to(torch.bfloat16).to(DEV) for _ in range(3)]
+    q, k, v = (t.transpose(-1, -2) for t in base)
+    assert q.stride(-1) != 1
+    do = torch.randn(B, H, N, D, generator=g).to(torch.bfloat16).to(DEV)
+    table = CosSinTable(ROPE_BASE, side, D, device=DEV)
+    ours = _run_ours(q, k, v, do, table, True)
+    ref = _ref(q, k, v, do, table, True)
+    _compare("tail-d-strided", ours, ref, out_dtype=torch.bfloat16)
+
+    q, k, v = (t.contiguous() for t in (q, k, v))
+    rope = table.packed()
+    scale = 1 / math.sqrt(D)
+    o, lse, res = torch.ops.farope.attn_fwd(q, k, v, rope, N - 1, True, scale, _lib.BF16)
+    dq, dk, dv = torch.ops.farope.attn_bwd(do, q, k, v, o, lse, rope, N - 1, True, scale, _lib.BF16, res)
+    desc = _lib.make_desc(B, H, N, D, N - 1, True, _lib.BF16, _lib.BF16, scale)
+    delta = torch.empty(B, H, N, device=DEV, dtype=torch.float32)
+    dq2, dk2, dv2 = (torch.empty_like(q) for _ in range(3))
+    _lib.attn_bwd_preprocess(desc, o, do, delta, res)
+    _lib.attn_bwd_dk_dv(desc, q, k, v, do, lse, delta, rope, dk2, dv2)
+    _lib.attn_bwd_dq(desc, q, k, v, do, lse, delta, rope, dq2)
+    torch.cuda.synchronize()
+    for name, a, b in (("dQ", dq2, dq), ("dK", dk2, dk), ("dV", dv2, dv)):
+        mx, _ = errors(a, b)
+        _say(f"[tail split-vs-one-call] {name}: max diff {mx:.3e}")
+        assert mx < 1e-2
+
+
 def test_strided_qkv_views():
     """q/k/v as permuted views of one [B, N, 3, H, D] projection (ViT attention layout)."""
     B, H, side, D = 4, 12, 14, 64

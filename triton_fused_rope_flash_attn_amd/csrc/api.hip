@@ -149,6 +149,29 @@ int scratch_ptr(float** out) {
   return FAROPE_OK;
 }
 
+// Block count for N rows in blocks of `rows`; with a tail, full blocks only.
+int main_blocks(int N, int rows) { return tail_rows(N, rows) ? N / rows : cdiv(N, rows); }
+
+// dQ block kernel (+ the tail rows kernel); with write_delta both write delta
+int dq_pass(BwdParams p, const farope_attn_desc* d, bool write_delta, hipStream_t st) {
+  const int D = d->head_dim, rows = bwd_dq_block_rows(D, d->compute_dtype);
+  const int tail = tail_rows(p.N, rows);
+  p.n_blk = main_blocks(p.N, rows);
+  FAROPE_TRY(launch_rc(launch_bwd_dq(p, d->io_dtype, d->compute_dtype, D, write_delta, st)));
+  if (tail) FAROPE_TRY(launch_rc(launch_bwd_tail_rows(p, d->io_dtype, D, p.N - tail, write_delta, st)));
+  return FAROPE_OK;
+}
+
+// dK/dV block kernel (+ the tail keys kernel)
+int dkdv_pass(BwdParams p, const farope_attn_desc* d, hipStream_t st) {
+  const int D = d->head_dim, rows = bwd_dkdv_block_rows(D, d->compute_dtype);
+  const int tail = tail_rows(p.N, rows);
+  p.n_blk = main_blocks(p.N, rows);
+  FAROPE_TRY(launch_rc(launch_bwd_dkdv(p, d->io_dtype, d->compute_dtype, D, st)));
+  if (tail) FAROPE_TRY(launch_rc(launch_bwd_tail_keys(p, d->io_dtype, D, p.N - tail, st)));
+  return FAROPE_OK;
+}
+
 int bwd_impl(const farope_attn_desc* desc, const void* q, const int64_t q_stride[4],
              const void* k, const int64_t k_stride[4], const void* v, const int64_t v_stride[4],
              const void* o, const int64_t o_stride[4], const void* o_res, const void* dout,
@@ -202,10 +225,9 @@ int bwd_impl(const farope_attn_desc* desc, const void* q, const int64_t q_stride
     p.n_blk = 1;
     return launch_rc(launch_bwd_fused(p, desc->io_dtype, desc->compute_dtype, st));
   }
-  p.n_blk = cdiv(p.N, bwd_dq_block_rows(D, desc->compute_dtype));
-  FAROPE_TRY(launch_rc(launch_bwd_dq(p, desc->io_dtype, desc->compute_dtype, D, true, st)));
-  p.n_blk = cdiv(p.N, bwd_dkdv_block_rows(D, desc->compute_dtype));
-  return launch_rc(launch_bwd_dkdv(p, desc->io_dtype, desc->compute_dtype, D, st));
+  // dQ (and delta, which the dK/dV pass reads for every row) before dK / dV
+  FAROPE_TRY(dq_pass(p, desc, true, st));
+  return dkdv_pass(p, desc, st);
 }
 
 }  // namespace
@@ -257,13 +279,13 @@ int farope_tile_config(const farope_attn_desc* desc, int32_t which, int32_t out[
     const int rows = fwd_block_rows(D);
     out[0] = 0;
     out[1] = rows;
-    out[2] = cdiv(N, rows);
+    out[2] = main_blocks(N, rows);
     out[3] = fwd_threads(D);
   } else {
     const bool fu = bwd_fused(desc);
     out[0] = fu ? BWD_FUSED : BWD_SPLIT;
     out[1] = fu ? bwd_fused_rows() : bwd_dkdv_block_rows(D, desc->compute_dtype);
-    out[2] = cdiv(N, out[1]);
+    out[2] = fu ? cdiv(N, out[1]) : main_blocks(N, out[1]);
     out[3] = fu ? 512 : bwd_dkdv_threads(D, desc->compute_dtype);
   }
   return FAROPE_OK;
@@ -301,10 +323,13 @@ int farope_attn_fwd(const farope_attn_desc* desc, const void* q, const int64_t q
   p.vec_k = vec_ok(k, k_stride, es, desc->seq_len, desc->head_dim);
   p.vec_v = vec_ok(v, v_stride, es, desc->seq_len, desc->head_dim);
   p.vec_o = vec_out_ok(o, o_stride, es, desc->seq_len, desc->head_dim);
-  p.n_blk = cdiv(p.N, fwd_block_rows(desc->head_dim));
+  const int rows = fwd_block_rows(desc->head_dim), tail = tail_rows(p.N, rows);
+  p.n_blk = main_blocks(p.N, rows);
   p.n_items = p.B * p.H * p.n_blk;
-  return launch_rc(launch_fwd(p, desc->io_dtype, desc->compute_dtype, desc->head_dim,
-                              static_cast<hipStream_t>(stream)));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  FAROPE_TRY(launch_rc(launch_fwd(p, desc->io_dtype, desc->compute_dtype, desc->head_dim, st)));
+  if (tail) FAROPE_TRY(launch_rc(launch_fwd_tail(p, desc->io_dtype, desc->head_dim, p.N - tail, st)));
+  return FAROPE_OK;
 }
 
 int farope_attn_bwd_preprocess(const farope_attn_desc* desc, const void* o,
@@ -359,9 +384,7 @@ int farope_attn_bwd_dk_dv(const farope_attn_desc* desc, const void* q, const int
   p.vec_do = vec_ok(dout, dout_stride, es, desc->seq_len, desc->head_dim);
   p.vec_dk = vec_out_ok(dk, dk_stride, es, desc->seq_len, desc->head_dim);
   p.vec_dv = vec_out_ok(dv, dv_stride, es, desc->seq_len, desc->head_dim);
-  p.n_blk = cdiv(p.N, bwd_dkdv_block_rows(desc->head_dim, desc->compute_dtype));
-  return launch_rc(launch_bwd_dkdv(p, desc->io_dtype, desc->compute_dtype, desc->head_dim,
-                                   static_cast<hipStream_t>(stream)));
+  return dkdv_pass(p, desc, static_cast<hipStream_t>(stream));
 }
 
 int farope_attn_bwd_dq(const farope_attn_desc* desc, const void* q, const int64_t q_stride[4],
@@ -391,9 +414,7 @@ int farope_attn_bwd_dq(const farope_attn_desc* desc, const void* q, const int64_
   p.vec_v = vec_ok(v, v_stride, es, desc->seq_len, desc->head_dim);
   p.vec_do = vec_ok(dout, dout_stride, es, desc->seq_len, desc->head_dim);
   p.vec_dq = vec_out_ok(dq, dq_stride, es, desc->seq_len, desc->head_dim);
-  p.n_blk = cdiv(p.N, bwd_dq_block_rows(desc->head_dim, desc->compute_dtype));
-  return launch_rc(launch_bwd_dq(p, desc->io_dtype, desc->compute_dtype, desc->head_dim, false,
-                                 static_cast<hipStream_t>(stream)));
+  return dq_pass(p, desc, false, static_cast<hipStream_t>(stream));
 }
 
 int farope_attn_bwd(const farope_attn_desc* desc, const void* q, const int64_t q_stride[4],

@@ -66,6 +66,17 @@ hipError_t launch_rope_pack(const float* cosp, int64_t cs0, int64_t cs1, const f
                             int64_t ss0, int64_t ss1, int n_pos, int d2, float* out,
                             hipStream_t st);
 
+// Tail rows (tail.hip): when 0 < N % block_rows <= kTailMaxRows and N >= block_rows,
+// the block kernels cover the full blocks only and these kernels compute the
+// last tail_rows(N, block_rows) rows (forward: O, LSE; rows: dQ and, with
+// write_delta, delta; keys: dK, dV) -- rows [row0, N) of every plane.
+constexpr int kTailMaxRows = 8;
+int tail_rows(int N, int block_rows);
+hipError_t launch_fwd_tail(const FwdParams& p, int io, int D, int row0, hipStream_t st);
+hipError_t launch_bwd_tail_rows(const BwdParams& p, int io, int D, int row0, bool write_delta,
+                                hipStream_t st);
+hipError_t launch_bwd_tail_keys(const BwdParams& p, int io, int D, int key0, hipStream_t st);
+
 // Split-operand ("precise") logits and dS: bf16 compute at head_dim >= 128.
 // Rounding the rotated Q / K rows to bf16 before the logits product is the
 // dominant error of bf16 attention there (long, wide planes with large
