@@ -149,14 +149,23 @@ int scratch_ptr(float** out) {
   return FAROPE_OK;
 }
 
+// Rows left to the tail kernels (0: none).  Their grid holds one workgroup
+// per (plane, row), so it must stay within the 2^31 - 1 grid limit.
+int tail_of(int planes, int N, int rows) {
+  const int t = tail_rows(N, rows);
+  return (int64_t)planes * t <= INT32_MAX ? t : 0;
+}
+
 // Block count for N rows in blocks of `rows`; with a tail, full blocks only.
-int main_blocks(int N, int rows) { return tail_rows(N, rows) ? N / rows : cdiv(N, rows); }
+int main_blocks(int planes, int N, int rows) {
+  return tail_of(planes, N, rows) ? N / rows : cdiv(N, rows);
+}
 
 // dQ block kernel (+ the tail rows kernel); with write_delta both write delta
 int dq_pass(BwdParams p, const farope_attn_desc* d, bool write_delta, hipStream_t st) {
   const int D = d->head_dim, rows = bwd_dq_block_rows(D, d->compute_dtype);
-  const int tail = tail_rows(p.N, rows);
-  p.n_blk = main_blocks(p.N, rows);
+  const int tail = tail_of(p.B * p.H, p.N, rows);
+  p.n_blk = main_blocks(p.B * p.H, p.N, rows);
   FAROPE_TRY(launch_rc(launch_bwd_dq(p, d->io_dtype, d->compute_dtype, D, write_delta, st)));
   if (tail) FAROPE_TRY(launch_rc(launch_bwd_tail_rows(p, d->io_dtype, D, p.N - tail, write_delta, st)));
   return FAROPE_OK;
@@ -165,8 +174,8 @@ int dq_pass(BwdParams p, const farope_attn_desc* d, bool write_delta, hipStream_
 // dK/dV block kernel (+ the tail keys kernel)
 int dkdv_pass(BwdParams p, const farope_attn_desc* d, hipStream_t st) {
   const int D = d->head_dim, rows = bwd_dkdv_block_rows(D, d->compute_dtype);
-  const int tail = tail_rows(p.N, rows);
-  p.n_blk = main_blocks(p.N, rows);
+  const int tail = tail_of(p.B * p.H, p.N, rows);
+  p.n_blk = main_blocks(p.B * p.H, p.N, rows);
   FAROPE_TRY(launch_rc(launch_bwd_dkdv(p, d->io_dtype, d->compute_dtype, D, st)));
   if (tail) FAROPE_TRY(launch_rc(launch_bwd_tail_keys(p, d->io_dtype, D, p.N - tail, st)));
   return FAROPE_OK;
@@ -279,13 +288,13 @@ int farope_tile_config(const farope_attn_desc* desc, int32_t which, int32_t out[
     const int rows = fwd_block_rows(D);
     out[0] = 0;
     out[1] = rows;
-    out[2] = main_blocks(N, rows);
+    out[2] = main_blocks(desc->batch * desc->heads, N, rows);
     out[3] = fwd_threads(D);
   } else {
     const bool fu = bwd_fused(desc);
     out[0] = fu ? BWD_FUSED : BWD_SPLIT;
     out[1] = fu ? bwd_fused_rows() : bwd_dkdv_block_rows(D, desc->compute_dtype);
-    out[2] = fu ? cdiv(N, out[1]) : main_blocks(N, out[1]);
+    out[2] = fu ? cdiv(N, out[1]) : main_blocks(desc->batch * desc->heads, N, out[1]);
     out[3] = fu ? 512 : bwd_dkdv_threads(D, desc->compute_dtype);
   }
   return FAROPE_OK;
@@ -323,8 +332,8 @@ int farope_attn_fwd(const farope_attn_desc* desc, const void* q, const int64_t q
   p.vec_k = vec_ok(k, k_stride, es, desc->seq_len, desc->head_dim);
   p.vec_v = vec_ok(v, v_stride, es, desc->seq_len, desc->head_dim);
   p.vec_o = vec_out_ok(o, o_stride, es, desc->seq_len, desc->head_dim);
-  const int rows = fwd_block_rows(desc->head_dim), tail = tail_rows(p.N, rows);
-  p.n_blk = main_blocks(p.N, rows);
+  const int rows = fwd_block_rows(desc->head_dim), tail = tail_of(p.B * p.H, p.N, rows);
+  p.n_blk = main_blocks(p.B * p.H, p.N, rows);
   p.n_items = p.B * p.H * p.n_blk;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   FAROPE_TRY(launch_rc(launch_fwd(p, desc->io_dtype, desc->compute_dtype, desc->head_dim, st)));
