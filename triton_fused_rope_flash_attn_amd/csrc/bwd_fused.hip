@@ -379,7 +379,12 @@ bwd_plane_kernel(const BwdParams p) {
   //      choice between sweep variants makes the compiler copy all of them at
   //      the join every stage), and a wave with one live subtile shares its
   //      SIMD with a fully loaded one anyway. ----
-  auto sweep_keys = [&](int buf) __attribute__((always_inline)) {
+  // live1: some query of the stage's second 16-row half is below N.  When
+  // none is (the last stage of N = 193 .. 208, ViT-S/B), that half's S / dP
+  // products and probabilities are skipped: its P and dS fragment slots are
+  // zero for the dV / dK products, and its dS^T columns are left as they are,
+  // because they only reach dQ rows >= N, which are never stored.
+  auto sweep_keys = [&](int buf, bool live1) __attribute__((always_inline)) {
     constexpr int NUA = 2;
     const S* q = &sQ[buf][0];
     const S* g = &sG[buf][0];
@@ -388,6 +393,16 @@ bwd_plane_kernel(const BwdParams p) {
       Frag pf[NUA], dsf[NUA];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
+        if (h == 1 && !live1) {
+#pragma unroll
+          for (int u = 0; u < NUA; ++u) {
+            C::set2(pf[u], 2, 0.f, 0.f);
+            C::set2(pf[u], 3, 0.f, 0.f);
+            C::set2(dsf[u], 2, 0.f, 0.f);
+            C::set2(dsf[u], 3, 0.f, 0.f);
+          }
+          continue;
+        }
         const int q0 = 16 * h + 4 * lg;   // queries q0 .. q0+3 in this lane
         const f32x4 nl2 = *reinterpret_cast<const f32x4*>(&sL2[buf][q0]);   // -LSE * log2(e)
         const f32x4 ndl = *reinterpret_cast<const f32x4*>(&sDl[buf][q0]);   // -delta
@@ -509,7 +524,7 @@ bwd_plane_kernel(const BwdParams p) {
         prefetch(tp, rs, last ? 0 : qb + QS);
       }
       if constexpr (!FIRST) dq(plane, rdq, st - 1, buf ^ 1);
-      if (nu > 0) sweep_keys(buf);
+      if (nu > 0) sweep_keys(buf, qb + 16 < N);
     };
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
