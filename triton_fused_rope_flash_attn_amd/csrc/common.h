@@ -393,12 +393,22 @@ template <> struct Comp<DT_F32> {
 // dropped a_lo.b_lo is below the fp32 accumulation error); with one operand
 // split only, as a_hi.b_hi + a_hi.b_lo.
 // ---------------------------------------------------------------------------
+// Pairs: one packed conversion rounds both values; their fp32 images are the
+// packed word's low half shifted up and its high half masked (bf16 is the top
+// half of an fp32), so hi, lo of two values cost 6 VALU instructions.
 __device__ __forceinline__ void split_bf16x8(const float (&x)[8], bf16x8& hi, bf16x8& lo) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef bf16 b2 __attribute__((ext_vector_type(2)));
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const bf16 h = (bf16)x[e];
-    hi[e] = h;
-    lo[e] = (bf16)(x[e] - (float)h);
+  for (int p = 0; p < 4; ++p) {
+    const b2 h = __builtin_convertvector(f2{x[2 * p], x[2 * p + 1]}, b2);
+    const unsigned u = __builtin_bit_cast(unsigned, h);
+    const float h0 = __uint_as_float(u << 16), h1 = __uint_as_float(u & 0xffff0000u);
+    const b2 l = __builtin_convertvector(f2{x[2 * p] - h0, x[2 * p + 1] - h1}, b2);
+    hi[2 * p] = h[0];
+    hi[2 * p + 1] = h[1];
+    lo[2 * p] = l[0];
+    lo[2 * p + 1] = l[1];
   }
 }
 
