@@ -150,10 +150,14 @@ bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = g[e] = 0.f;
       }
-      if constexpr (PS)
+      if constexpr (PS) {
+        // split operands: Q-hat carries the logit scale (see put_khat)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] *= p.scale_log2;
         split_bf16x8(x, qf[t][s].v, qfl[t][s].v);
-      else
+      } else {
         qf[t][s] = C::make(x);
+      }
       gf[t][s] = C::make(g);
     }
     if (WRITE_DELTA) {
@@ -166,7 +170,8 @@ bwd_dq_kernel(const BwdParams p) {
     lse2[t] = row < N ? p.lse[prow + row] * kLog2e : 0.f;
   }
   const bool wave_active = qblk * QROWS + wave * QT * 16 < N;
-  const float dq_scale = p.scale / p.scale_log2;   // K-hat is staged pre-scaled by scale * log2(e)
+  // K-hat is staged pre-scaled by scale * log2(e) (split operands: unscaled)
+  const float dq_scale = PS ? p.scale : p.scale / p.scale_log2;
 
   f32x4 dqacc[QT][DT];
 #pragma unroll
@@ -176,10 +181,15 @@ bwd_dq_kernel(const BwdParams p) {
 
   // K-hat row segment -> sK (PS: hi to sK, lo to sKl), pre-scaled by
   // softmax_scale * log2(e) as in the forward pass, so that both passes see
-  // bit-identical logits in log2 units (dQ's scale divides it out again)
+  // bit-identical logits in log2 units (dQ's scale divides it out again).
+  // With split operands the forward and this kernel scale Q-hat instead (it
+  // is staged once, K-hat once per stage) and the dK/dV kernel K-hat (staged
+  // once): the split roundings agree to about 2^-16, so the passes' logits do.
   auto put_khat = [&](int off, float (&xk)[8]) __attribute__((always_inline)) {
+    if constexpr (!PS) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) xk[e] *= p.scale_log2;
+      for (int e = 0; e < 8; ++e) xk[e] *= p.scale_log2;
+    }
     if constexpr (PS) {
       bf16x8 hi, lo;
       split_bf16x8(xk, hi, lo);
@@ -541,9 +551,9 @@ bwd_dkdv_kernel(const BwdParams p) {
           }
         }
       }
-      if (tid < QS) {
-        sL2[tid] = qb + tid < N ? pl * kLog2e : INFINITY;
-        sDl[tid] = qb + tid < N ? pd : 0.f;
+      if (tid < QS) {   // negated: they seed the S and dP accumulators
+        sL2[tid] = qb + tid < N ? -pl * kLog2e : -INFINITY;
+        sDl[tid] = qb + tid < N ? -pd : 0.f;
       }
     }
   };
@@ -592,29 +602,26 @@ bwd_dkdv_kernel(const BwdParams p) {
       }
       for (int r = tid; r < rows; r += NT) {
         const int gr = qb + r;
-        sL2[r] = gr < N ? p.lse[prow + gr] * kLog2e : INFINITY;
-        sDl[r] = gr < N ? p.delta[prow + gr] : 0.f;
+        sL2[r] = gr < N ? -p.lse[prow + gr] * kLog2e : -INFINITY;
+        sDl[r] = gr < N ? -p.delta[prow + gr] : 0.f;
       }
     }
     lds_barrier();
     }
 
     for (int j = 0; j < rows / 32; ++j) {
-      float l2[8], dl[8];
-      {
-        const f32x4 a = *reinterpret_cast<const f32x4*>(&sL2[32 * j + 8 * lg]);
-        const f32x4 b = *reinterpret_cast<const f32x4*>(&sL2[32 * j + 8 * lg + 4]);
-        const f32x4 c = *reinterpret_cast<const f32x4*>(&sDl[32 * j + 8 * lg]);
-        const f32x4 d = *reinterpret_cast<const f32x4*>(&sDl[32 * j + 8 * lg + 4]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) { l2[e] = a[e]; l2[4 + e] = b[e]; dl[e] = c[e]; dl[4 + e] = d[e]; }
-      }
+      // -LSE2 and -delta of queries 32j + 8lg + e, e = 4h + i: the S and dP
+      // accumulator seeds of half h (P = exp2(S), dP - delta need no
+      // arithmetic; queries >= N have -LSE2 = -inf, so P = 0)
+      const f32x4 nl2[2] = {*reinterpret_cast<const f32x4*>(&sL2[32 * j + 8 * lg]),
+                            *reinterpret_cast<const f32x4*>(&sL2[32 * j + 8 * lg + 4])};
+      const f32x4 ndl[2] = {*reinterpret_cast<const f32x4*>(&sDl[32 * j + 8 * lg]),
+                            *reinterpret_cast<const f32x4*>(&sDl[32 * j + 8 * lg + 4])};
 #pragma unroll
       for (int u = 0; u < KT; ++u) {
         const int kv0 = kv_first + 16 * u;
         if (kv0 >= N) continue;   // wave-uniform
-        f32x4 sacc[2], pacc[2];
-        sacc[0] = sacc[1] = pacc[0] = pacc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 sacc[2] = {nl2[0], nl2[1]}, pacc[2] = {ndl[0], ndl[1]};
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
 #pragma unroll
@@ -631,16 +638,18 @@ bwd_dkdv_kernel(const BwdParams p) {
             pacc[h] = C::mma(b, vf[u][s], pacc[h]);
           }
         }
-        const bool kvalid = kv0 + lr < N;
+        // Keys >= N (lane key kv0 + lr) need no mask: their K-hat and V rows
+        // are zero, so P and dS there are finite and only reach the dK / dV
+        // rows of those keys, which are never stored.
         float pv[8], dsv[8];
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int e = 4 * h + i;
-            const float pr = kvalid ? fast_exp2(sacc[h][i] - l2[e]) : 0.f;
+            const float pr = fast_exp2(sacc[h][i]);
             pv[e] = pr;
-            dsv[e] = pr * (pacc[h][i] - dl[e]);
+            dsv[e] = pr * pacc[h][i];
           }
         const Frag pf = C::make(pv);
         Frag dsf, dsfl;

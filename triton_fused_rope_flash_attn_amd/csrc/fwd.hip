@@ -281,9 +281,13 @@ fwd_kernel(const FwdParams p) {
           }
           // K-hat pre-scaled by softmax_scale * log2(e): the logits come out
           // of the MFMAs in log2 units (every kernel stages K-hat this way, so
-          // the forward and backward passes see bit-identical logits)
+          // the forward and backward passes see bit-identical logits).  With
+          // split operands Q-hat carries the scale instead: it is staged once
+          // per item, K-hat once per chunk.
+          if constexpr (!PS) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) xk[e] *= c2;
+            for (int e = 0; e < 8; ++e) xk[e] *= c2;
+          }
           if constexpr (PS) {
             bf16x8 hi, lo;
             split_bf16x8(xk, hi, lo);
@@ -367,10 +371,13 @@ fwd_kernel(const FwdParams p) {
         } else {
           rope_rotate8(x, qcs[t][s]);
         }
-        if constexpr (PS)
+        if constexpr (PS) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] *= c2;
           split_bf16x8(x, qf[t][s].v, qfl[t][s].v);
-        else
+        } else {
           qf[t][s] = C::make(x);
+        }
       }
   };
 
