@@ -24,6 +24,9 @@
 //    other side of the plane for every workgroup, so workgroups are 8 waves
 //    wide (BwdShape), and with vector-accessible inputs the next stage's raw
 //    rows are prefetched into registers while the current one is computed.
+//  * When 1 to 8 rows (keys) are left past the last full block, the launcher
+//    runs these kernels over the full blocks only and tail.hip computes the
+//    rest.
 #include <type_traits>
 
 #include "common.h"
