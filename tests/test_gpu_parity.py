@@ -196,13 +196,13 @@ def test_ragged_and_variant_shapes(side, has_cls, D):
 def test_tail_rows(side, has_cls, D, B, H, io):
     """Rows past the last full block (N % block_rows <= 8, e.g. N = 16^2 + 1, 63^2 + 1,
     62^2): computed by the tail kernels, not by a nearly empty block.  One tail row at
-    every head dim and I/O type; two (N = 3970) and four (N = 3844, no CLS) rows."""
+    every head dim and I/O type; two (N = 3970, dK/dV) and four (N = 3844, no CLS) rows."""
     dt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[io]
     N = side * side + int(has_cls)
     code = _lib.DTYPE_CODE[dt]
     desc = _lib.make_desc(B, H, N, D, N - int(has_cls), has_cls, code, code, 1 / math.sqrt(D))
-    rows = _lib.tile_config(desc, 0)[1]   # forward block rows
-    assert N >= rows and 0 < N % rows <= 8
+    rows = (_lib.tile_config(desc, 0)[1], _lib.tile_config(desc, 1)[1])   # forward, dK/dV block rows
+    assert any(N >= r and 0 < N % r <= 8 for r in rows)
     cfg = dict(B=B, H=H, side=side, has_cls=has_cls, D=D, dtype=dt, scale=1.0, dout="randn")
     q, k, v, do = make_inputs(cfg, DEV, seed=5)
     table = CosSinTable(ROPE_BASE, side, D, device=DEV)

@@ -285,7 +285,7 @@ int farope_tile_config(const farope_attn_desc* desc, int32_t which, int32_t out[
   if (!out) return FAROPE_ERR_NULL;
   const int D = desc->head_dim, N = desc->seq_len;
   if (which == 0) {
-    const int rows = fwd_block_rows(D);
+    const int rows = fwd_block_rows(D, desc->io_dtype, desc->compute_dtype);
     out[0] = 0;
     out[1] = rows;
     out[2] = main_blocks(desc->batch * desc->heads, N, rows);
@@ -332,7 +332,8 @@ int farope_attn_fwd(const farope_attn_desc* desc, const void* q, const int64_t q
   p.vec_k = vec_ok(k, k_stride, es, desc->seq_len, desc->head_dim);
   p.vec_v = vec_ok(v, v_stride, es, desc->seq_len, desc->head_dim);
   p.vec_o = vec_out_ok(o, o_stride, es, desc->seq_len, desc->head_dim);
-  const int rows = fwd_block_rows(desc->head_dim), tail = tail_of(p.B * p.H, p.N, rows);
+  const int rows = fwd_block_rows(desc->head_dim, desc->io_dtype, desc->compute_dtype);
+  const int tail = tail_of(p.B * p.H, p.N, rows);
   p.n_blk = main_blocks(p.B * p.H, p.N, rows);
   p.n_items = p.B * p.H * p.n_blk;
   const hipStream_t st = static_cast<hipStream_t>(stream);

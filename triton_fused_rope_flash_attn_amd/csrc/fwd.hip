@@ -319,9 +319,14 @@ fwd_kernel(const FwdParams p) {
   };
 
   // ---- Q rows of an item: raw prefetch registers -> rotated B-operand fragments ----
-  Raw8<IO> qraw[QT][KS];
-  float qcs[QT][KS][kTabLds ? 1 : 8];
+  // Split operands with two subtiles per wave load the rows when the item
+  // starts instead: their prefetch registers (rows and table values) would
+  // not fit beside the two subtiles' split Q-hat and O accumulators.
+  constexpr bool kQpf = !(PS && QT > 1);
+  Raw8<IO> qraw[kQpf ? QT : 1][kQpf ? KS : 1];
+  float qcs[kQpf ? QT : 1][kQpf ? KS : 1][kTabLds ? 1 : 8];
   auto prefetch_q = [&](int item) __attribute__((always_inline)) {
+    if constexpr (!kQpf) return;
     const int plane = item / p.n_blk, qb = item - plane * p.n_blk;
     if constexpr (VEC && kTabLds) {
       const auto rQ = rsrc(p.q, p.sq, plane);
@@ -356,12 +361,25 @@ fwd_kernel(const FwdParams p) {
   };
   Frag qf[QT][KS];
   Frag qfl[PS ? QT : 1][PS ? KS : 1];   // PS: Q-hat lo
-  auto commit_q = [&](int qb) __attribute__((always_inline)) {
+  auto commit_q = [&](int plane, int qb) __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < QT; ++t)
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         float x[8];
+        if constexpr (!kQpf) {
+          const int row = (qb * NW * QT + t * NW + wave) * 16 + lr;
+          const int c0 = 32 * s + 8 * lg;
+          float cs[8];
+          if (row < N) {
+            unpack8(load_raw8(plane_base(p.q, p.sq, plane) + row * p.sq[2] + c0 * p.sq[3], p.sq[3], vec_q), x);
+            rope_load4(p.rope, row + shift, D2, c0 / 2, cs);
+            rope_rotate8(x, cs);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = 0.f;
+          }
+        } else {
         unpack8(qraw[t][s], x);
         if constexpr (kTabLds) {
           const int row = (qb * NW * QT + t * NW + wave) * 16 + lr;
@@ -370,6 +388,7 @@ fwd_kernel(const FwdParams p) {
           rope_rotate8(x, cs);
         } else {
           rope_rotate8(x, qcs[t][s]);
+        }
         }
         if constexpr (PS) {
 #pragma unroll
@@ -724,7 +743,9 @@ fwd_kernel(const FwdParams p) {
   // drain.  The stores are unconditional: rows >= N fall outside the
   // descriptor range and are dropped, LSE lanes lg != 0 write past their
   // range, and before the first item the ranges are empty.
-  constexpr bool kDefer = VEC && sizeof(IO) == 2;
+  // (Not with Q rows loaded at the item start: those loads wait for the
+  // stores either way, and the deferred store registers would not fit.)
+  constexpr bool kDefer = VEC && sizeof(IO) == 2 && kQpf;
   u32x2 ost[kDefer ? QT : 1][DT];
   // RES: O's rounding residual bf16(O - bf16(O)) goes to p.o_res (contiguous
   // [B, H, N, D]) next to O, for the backward's delta; stored only when the
@@ -787,7 +808,7 @@ fwd_kernel(const FwdParams p) {
   while (item >= 0) {
     const int plane = item / p.n_blk, qb = item - plane * p.n_blk;
     const int nxt = item_of(it + 1);
-    commit_q(qb);
+    commit_q(plane, qb);
     int nt = 0;   // active subtiles of this wave: a prefix t < nt (wave-uniform)
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
@@ -955,9 +976,20 @@ template <> struct FwdShape<128> { static constexpr int NW = 8, QT = 1, KC = 64,
 // 512 registers (VGPRs plus AGPRs): the O accumulators alone are 64 per wave.
 template <> struct FwdShape<256> { static constexpr int NW = 4, QT = 1, KC = 32, TABROWS = 0; };
 
-template <int D> static int fwd_rows() { return FwdShape<D>::NW * FwdShape<D>::QT * 16; }
-int fwd_block_rows(int D) {
-  return D == 32 ? fwd_rows<32>() : D == 64 ? fwd_rows<64>() : D == 128 ? fwd_rows<128>() : fwd_rows<256>();
+// Query subtiles per wave: split-operand logits (bf16 compute, D = 128) with
+// 16-bit tensors take two, so that every staged K-hat chunk (rotated and
+// split per item) serves twice the queries; their Q rows then load at the
+// item start (no prefetch).  32-bit tensors need those registers for staging.
+template <int D, bool PS, bool IO16> constexpr int fwd_qt() {
+  return PS && IO16 && D == 128 ? 2 : FwdShape<D>::QT;
+}
+template <int D> static int fwd_rows_of(int io, int ct) {
+  const bool two = ct == DT_BF16 && io != DT_F32 && precise_logits(DT_BF16, D);
+  return FwdShape<D>::NW * (two ? fwd_qt<D, true, true>() : FwdShape<D>::QT) * 16;
+}
+int fwd_block_rows(int D, int io, int ct) {
+  return D == 32 ? fwd_rows_of<32>(io, ct) : D == 64 ? fwd_rows_of<64>(io, ct)
+         : D == 128 ? fwd_rows_of<128>(io, ct) : fwd_rows_of<256>(io, ct);
 }
 int fwd_threads(int D) {
   return 64 * (D == 32    ? FwdShape<32>::NW
@@ -975,12 +1007,13 @@ static hipError_t fwd_launch(const FwdParams& p0, hipStream_t st) {
   // split-operand logits for bf16 compute at head_dim >= 128 (the backward's
   // split kernels use the same rule, so both passes see the same S)
   constexpr bool PS = precise_logits(CT, D);
+  constexpr int QT = fwd_qt<D, PS, sizeof(IO) == 2>();
   const bool tab = TR > 0 && p.N + 1 - p.has_cls <= TR;
   const bool vec = p.vec_q && p.vec_k && p.vec_v && p.vec_o;
-  auto kern = tab ? (vec ? fwd_kernel<IO, CT, D, SH::NW, SH::QT, SH::KC, TR, true, PS>
-                         : fwd_kernel<IO, CT, D, SH::NW, SH::QT, SH::KC, TR, false, PS>)
-                  : (vec ? fwd_kernel<IO, CT, D, SH::NW, SH::QT, SH::KC, 0, true, PS>
-                         : fwd_kernel<IO, CT, D, SH::NW, SH::QT, SH::KC, 0, false, PS>);
+  auto kern = tab ? (vec ? fwd_kernel<IO, CT, D, SH::NW, QT, SH::KC, TR, true, PS>
+                         : fwd_kernel<IO, CT, D, SH::NW, QT, SH::KC, TR, false, PS>)
+                  : (vec ? fwd_kernel<IO, CT, D, SH::NW, QT, SH::KC, 0, true, PS>
+                         : fwd_kernel<IO, CT, D, SH::NW, QT, SH::KC, 0, false, PS>);
   const int grid = persistent_grid(reinterpret_cast<const void*>(kern), SH::NW * 64, p.n_items);
   if (grid <= 0) return hipErrorInvalidConfiguration;
   p.n_wg = grid;

@@ -94,7 +94,7 @@ constexpr bool o_residual(int io, int ct, int D) { return io == 2 && precise_log
 int persistent_grid(const void* kernel, int block_threads, int items, size_t dyn_lds = 0);
 
 // Rows of q (fwd, dq) or kv (dk/dv) one work item / workgroup covers.
-int fwd_block_rows(int D);
+int fwd_block_rows(int D, int io, int ct);
 int fwd_threads(int D);
 int bwd_dq_block_rows(int D, int ct);
 int bwd_dkdv_block_rows(int D, int ct);
