@@ -319,10 +319,11 @@ fwd_kernel(const FwdParams p) {
   };
 
   // ---- Q rows of an item: raw prefetch registers -> rotated B-operand fragments ----
-  // Split operands with two subtiles per wave load the rows when the item
-  // starts instead: their prefetch registers (rows and table values) would
-  // not fit beside the two subtiles' split Q-hat and O accumulators.
-  constexpr bool kQpf = !(PS && QT > 1);
+  // At D = 128 with two subtiles per wave, or with split operands and 32-bit
+  // tensors, the rows load when the item starts instead: the prefetch
+  // registers (rows and table values) would not fit beside the Q-hat
+  // fragments and O accumulators.
+  constexpr bool kQpf = !(D == 128 && (QT > 1 || (PS && sizeof(IO) == 4)));
   Raw8<IO> qraw[kQpf ? QT : 1][kQpf ? KS : 1];
   float qcs[kQpf ? QT : 1][kQpf ? KS : 1][kTabLds ? 1 : 8];
   auto prefetch_q = [&](int item) __attribute__((always_inline)) {
@@ -976,16 +977,17 @@ template <> struct FwdShape<128> { static constexpr int NW = 8, QT = 1, KC = 64,
 // 512 registers (VGPRs plus AGPRs): the O accumulators alone are 64 per wave.
 template <> struct FwdShape<256> { static constexpr int NW = 4, QT = 1, KC = 32, TABROWS = 0; };
 
-// Query subtiles per wave: split-operand logits (bf16 compute, D = 128) with
-// 16-bit tensors take two, so that every staged K-hat chunk (rotated and
-// split per item) serves twice the queries; their Q rows then load at the
-// item start (no prefetch).  32-bit tensors need those registers for staging.
-template <int D, bool PS, bool IO16> constexpr int fwd_qt() {
-  return PS && IO16 && D == 128 ? 2 : FwdShape<D>::QT;
+// Query subtiles per wave at D = 128: two with 16-bit tensors and 16-bit
+// compute, so that every staged K-hat chunk (rotated, and split with
+// split-operand logits, once per item) serves twice the queries; their Q rows
+// then load at the item start (no prefetch).  32-bit tensors or compute need
+// those registers for staging.
+template <int D, int CT, bool IO16> constexpr int fwd_qt() {
+  return IO16 && CT != DT_F32 && D == 128 ? 2 : FwdShape<D>::QT;
 }
 template <int D> static int fwd_rows_of(int io, int ct) {
-  const bool two = ct == DT_BF16 && io != DT_F32 && precise_logits(DT_BF16, D);
-  return FwdShape<D>::NW * (two ? fwd_qt<D, true, true>() : FwdShape<D>::QT) * 16;
+  const bool two = io != DT_F32 && ct != DT_F32;
+  return FwdShape<D>::NW * (two ? fwd_qt<D, DT_BF16, true>() : FwdShape<D>::QT) * 16;
 }
 int fwd_block_rows(int D, int io, int ct) {
   return D == 32 ? fwd_rows_of<32>(io, ct) : D == 64 ? fwd_rows_of<64>(io, ct)
@@ -1007,7 +1009,7 @@ static hipError_t fwd_launch(const FwdParams& p0, hipStream_t st) {
   // split-operand logits for bf16 compute at head_dim >= 128 (the backward's
   // split kernels use the same rule, so both passes see the same S)
   constexpr bool PS = precise_logits(CT, D);
-  constexpr int QT = fwd_qt<D, PS, sizeof(IO) == 2>();
+  constexpr int QT = fwd_qt<D, CT, sizeof(IO) == 2>();
   const bool tab = TR > 0 && p.N + 1 - p.has_cls <= TR;
   const bool vec = p.vec_q && p.vec_k && p.vec_v && p.vec_o;
   auto kern = tab ? (vec ? fwd_kernel<IO, CT, D, SH::NW, QT, SH::KC, TR, true, PS>
