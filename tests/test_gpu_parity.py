@@ -390,6 +390,48 @@ def test_large_logits_finite():
         assert mn <= 1.25 * omn + 1e-4, name
 
 
+@pytest.mark.parametrize("planes", [
+    # (q scale, k scale) per (b, h) plane: 2^20 / 2^-20 push |Q-hat| (with the
+    # logit scale) far past 2^12 and |K-hat| into fp16's subnormal range, and
+    # the reverse makes K-hat overflow fp16; the logits themselves stay those
+    # of unit inputs.  2^11 / 2^-11 stays below the rescale threshold.
+    [(2.0 ** 20, 2.0 ** -20), (1.0, 1.0), (2.0 ** -20, 2.0 ** 20), (2.0 ** 11, 2.0 ** -11)],
+], ids=["mixed"])
+def test_f16_logit_operand_range(planes):
+    """bf16 compute at head_dim 128 takes the logits from fp16 operands; a tile
+    whose Q-hat or K-hat reaches 2^12 is computed again with both operands
+    rescaled by powers of two.  With Q = a q0, K = k0 / a the logits are those
+    of (q0, k0), O and dV are unchanged, dQ scales by 1/a and dK by a: each
+    plane's outputs, divided by those factors, must meet the north-star
+    tolerance against the fp32 oracle on the same (scaled, bf16) inputs."""
+    B, H, side, D = 2, 2, 16, 128
+    N = side * side + 1
+    g = torch.Generator().manual_seed(3)
+    q, k, v, do = (torch.randn(B, H, N, D, generator=g) for _ in range(4))
+    fac = torch.ones(B, H, 4)
+    for i, (a, c) in enumerate(planes):
+        b, h = divmod(i, H)
+        q[b, h] *= a
+        k[b, h] *= c
+        fac[b, h] = torch.tensor([1.0, c, a, 1.0])   # O, dQ, dK, dV magnitude factors
+    q, k, v, do = (t.to(torch.bfloat16).to(DEV) for t in (q, k, v, do))
+    table = CosSinTable(ROPE_BASE, side, D, device=DEV)
+    ours = _run_ours(q, k, v, do, table, True)
+    ref = _ref(q, k, v, do, table, True)
+    fails = []
+    for i, name in enumerate(("O", "dQ", "dK", "dV")):
+        assert torch.isfinite(ours[i]).all(), name
+        for b in range(B):
+            for h in range(H):
+                f = fac[b, h, i].item()
+                mx, mn = errors(ours[i][b, h].float() / f, ref[i][b, h].float() / f)
+                _say(f"[fp16 range] plane ({b},{h}) scales {planes[b * H + h]} {name}/{f:g}: "
+                     f"max {mx:.3e} mean {mn:.3e}")
+                if mx > TOL_MAX or mn > TOL_MEAN:
+                    fails.append(f"plane ({b},{h}) {name}: max {mx:.3e} mean {mn:.3e}")
+    assert not fails, "; ".join(fails)
+
+
 def test_torch_compile_fullgraph():
     """The ops trace as opaque nodes: torch.compile(fullgraph=True) of the public
     entry (RoPE table packing included) matches eager bit for bit, fwd and bwd."""

@@ -75,15 +75,19 @@ __global__ void __launch_bounds__(256) bwd_pre_kernel(const BwdParams p) {
 // into registers while the current block is computed (buffer descriptors over
 // the plane, rows >= N read 0); their table rows are read when the block is
 // committed.  Otherwise each block is loaded synchronously.
-// PS (bf16 compute, head_dim >= 128): logits from split K-hat (LDS, hi + lo)
-// and Q-hat (registers, hi + lo) as in the forward pass, and dQ-hat from
-// dS = hi + lo: dQ-hat^T += K-hat^T dS_hi^T + K-hat^T dS_lo^T.
-template <typename IO, int CT, int D, int NW, int QT, int KVS, bool WRITE_DELTA, bool VEC, bool PS>
+// FS (bf16 compute, head_dim >= 128): logits from fp16 operands as in the
+// forward pass (an fp16 K-hat tile next to the bf16 one the dQ product
+// reads; Q-hat in registers), and dQ-hat from dS = hi + lo:
+// dQ-hat^T += K-hat^T dS_hi^T + K-hat^T dS_lo^T.  A tile whose Q-hat or
+// K-hat reaches 2^12 is computed again with scaled logit operands.
+template <typename IO, int CT, int D, int NW, int QT, int KVS, bool WRITE_DELTA, bool VEC, bool FS>
 __global__ void __launch_bounds__(NW * 64)
 bwd_dq_kernel(const BwdParams p) {
   using C = Comp<CT>;
   using S = typename C::S;
   using Frag = typename C::Frag;
+  using LC = std::conditional_t<FS, Comp<DT_F16>, C>;   // logits operands
+  using LFrag = typename LC::Frag;
   constexpr int KS = D / 32, DT = D / 16, D2 = D / 2;
   constexpr int PADE = 16 / sizeof(S);
   constexpr int LDK = D + PADE, LDT = KVS + PADE;
@@ -94,11 +98,12 @@ bwd_dq_kernel(const BwdParams p) {
   // fp32 storage keeps an explicit transposed copy.
   constexpr bool TR = sizeof(S) == 2;
 
-  static_assert(!PS || CT == DT_BF16, "split operands are bf16");
+  static_assert(!FS || CT == DT_BF16, "fp16 logit operands go with bf16 compute");
   __shared__ __attribute__((aligned(16))) S sK[KVS * LDK];
-  __shared__ __attribute__((aligned(16))) S sKl[PS ? KVS * LDK : 8];   // PS: K-hat lo
+  __shared__ __attribute__((aligned(16))) f16 sKf[FS ? KVS * LDK : 8];   // FS: fp16 K-hat
   __shared__ __attribute__((aligned(16))) S sKt[TR ? 8 : D * LDT];
   __shared__ __attribute__((aligned(16))) S sV[KVS * LDK];
+  __shared__ u32x2 sRange[FS ? NW : 1];   // FS: per-wave max |Q-hat|, |K-hat| bits
 
   const int N = p.N;
   const int tile = xcd_remap(block_id(), p.n_wg);
@@ -115,12 +120,21 @@ bwd_dq_kernel(const BwdParams p) {
   const int shift = 1 - p.has_cls;
   const int64_t prow = (int64_t)plane * N;
 
-  const int tid = thread_id();
+  // FS: largest |Q-hat| (scaled) and |K-hat| this thread converted in the
+  // current pass; the operand scales and the logit factor 1 / (fq fk) of a
+  // rescaled pass (all 1 otherwise)
+  float amax_q = 0.f, amax_k = 0.f;
+  float fq = 1.f, fk = 1.f, fsc = 1.f;
+  bool rescaled = false;
+  for (;;) {   // one pass, or two when FS rescales
+  // (FS: the lane index is opaque to the compiler, so that no lane-dependent
+  // address of the pass is hoisted out of this loop to hold registers)
+  const int tid = FS ? opaque(thread_id()) : thread_id();
   const int wave = tid >> 6, lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
 
-  Frag qf[QT][KS], gf[QT][KS];
-  Frag qfl[PS ? QT : 1][PS ? KS : 1];   // PS: Q-hat lo
+  LFrag qf[QT][KS];
+  Frag gf[QT][KS];
   float lse2[QT], dlt[QT];
   int qrow[QT];
 #pragma unroll
@@ -153,11 +167,13 @@ bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = g[e] = 0.f;
       }
-      if constexpr (PS) {
-        // split operands: Q-hat carries the logit scale (see put_khat)
+      if constexpr (FS) {
+        // fp16 operands: Q-hat carries the logit scale (see put_khat)
+        const float qs = p.scale_log2 * fq;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] *= p.scale_log2;
-        split_bf16x8(x, qf[t][s].v, qfl[t][s].v);
+        for (int e = 0; e < 8; ++e) x[e] *= qs;
+        amax_q = amax8(amax_q, x);
+        qf[t][s].v = to_f16x8(x);
       } else {
         qf[t][s] = C::make(x);
       }
@@ -172,9 +188,10 @@ bwd_dq_kernel(const BwdParams p) {
     }
     lse2[t] = row < N ? p.lse[prow + row] * kLog2e : 0.f;
   }
+  if constexpr (FS) amax_q = opaque(amax_q);
   const bool wave_active = qblk * QROWS + wave * QT * 16 < N;
-  // K-hat is staged pre-scaled by scale * log2(e) (split operands: unscaled)
-  const float dq_scale = PS ? p.scale : p.scale / p.scale_log2;
+  // K-hat is staged pre-scaled by scale * log2(e) (fp16 operands: unscaled)
+  const float dq_scale = FS ? p.scale : p.scale / p.scale_log2;
 
   f32x4 dqacc[QT][DT];
 #pragma unroll
@@ -182,24 +199,24 @@ bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
     for (int d = 0; d < DT; ++d) dqacc[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // K-hat row segment -> sK (PS: hi to sK, lo to sKl), pre-scaled by
-  // softmax_scale * log2(e) as in the forward pass, so that both passes see
-  // bit-identical logits in log2 units (dQ's scale divides it out again).
-  // With split operands the forward and this kernel scale Q-hat instead (it
-  // is staged once, K-hat once per stage) and the dK/dV kernel K-hat (staged
-  // once): the split roundings agree to about 2^-16, so the passes' logits do.
+  // K-hat row segment -> sK, pre-scaled by softmax_scale * log2(e) as in the
+  // forward pass, so that both passes see bit-identical logits in log2 units
+  // (dQ's scale divides it out again).  With fp16 operands every kernel
+  // scales Q-hat instead, and K-hat goes to sK unscaled in bf16 (the dQ
+  // product's operand) and to sKf in fp16 (times fk in a rescaled pass).
   auto put_khat = [&](int off, float (&xk)[8]) __attribute__((always_inline)) {
-    if constexpr (!PS) {
+    if constexpr (!FS) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) xk[e] *= p.scale_log2;
-    }
-    if constexpr (PS) {
-      bf16x8 hi, lo;
-      split_bf16x8(xk, hi, lo);
-      *reinterpret_cast<bf16x8*>(&sK[off]) = hi;
-      *reinterpret_cast<bf16x8*>(&sKl[off]) = lo;
+      C::put8(&sK[off], xk);
     } else {
       C::put8(&sK[off], xk);
+      if (rescaled) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xk[e] *= fk;
+      }
+      amax_k = amax8(amax_k, xk);
+      *reinterpret_cast<f16x8*>(&sKf[off]) = to_f16x8(xk);
     }
   };
 
@@ -329,24 +346,20 @@ bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const int kl = 32 * j + 8 * (lr >> 2) + 4 * h + (lr & 3);
-          const Frag a = C::lds(&sK[kl * LDK + 32 * s + 8 * lg]);
+          LFrag a;
+          if constexpr (FS)
+            a = LC::lds(&sKf[kl * LDK + 32 * s + 8 * lg]);
+          else
+            a = C::lds(&sK[kl * LDK + 32 * s + 8 * lg]);
           const Frag b = C::lds(&sV[kl * LDK + 32 * s + 8 * lg]);
-          if constexpr (PS) {
-            const Frag al = C::lds(&sKl[kl * LDK + 32 * s + 8 * lg]);
-#pragma unroll
-            for (int t = 0; t < QT; ++t) {
-              sacc[t][h] = C::mma(al, qf[t][s], sacc[t][h]);
-              sacc[t][h] = C::mma(a, qfl[t][s], sacc[t][h]);
-            }
-          }
 #pragma unroll
           for (int t = 0; t < QT; ++t) {
-            sacc[t][h] = C::mma(a, qf[t][s], sacc[t][h]);
+            sacc[t][h] = LC::mma(a, qf[t][s], sacc[t][h]);
             pacc[t][h] = C::mma(b, gf[t][s], pacc[t][h]);
           }
         }
       }
-      Frag dsf[QT], dsfl[PS ? QT : 1];
+      Frag dsf[QT], dsfl[FS ? QT : 1];
 #pragma unroll
       for (int t = 0; t < QT; ++t) {
         float ds[8];
@@ -354,8 +367,9 @@ bwd_dq_kernel(const BwdParams p) {
         for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            ds[4 * h + i] = fast_exp2(sacc[t][h][i] - lse2[t]) * pacc[t][h][i];
-        if constexpr (PS)
+            ds[4 * h + i] = fast_exp2(FS ? __builtin_fmaf(sacc[t][h][i], fsc, -lse2[t])
+                                         : sacc[t][h][i] - lse2[t]) * pacc[t][h][i];
+        if constexpr (FS)
           split_bf16x8(ds, dsf[t].v, dsfl[t].v);
         else
           dsf[t] = C::make(ds);
@@ -371,10 +385,37 @@ bwd_dq_kernel(const BwdParams p) {
           a = C::lds(&sKt[(16 * d + lr) * LDT + 32 * j + 8 * lg]);
 #pragma unroll
         for (int t = 0; t < QT; ++t) {
-          if constexpr (PS) dqacc[t][d] = C::mma(a, dsfl[t], dqacc[t][d]);
+          if constexpr (FS) dqacc[t][d] = C::mma(a, dsfl[t], dqacc[t][d]);
           dqacc[t][d] = C::mma(a, dsf[t], dqacc[t][d]);
         }
       }
+    }
+  }
+
+  if constexpr (FS) {
+    // Operand ranges of this pass over the workgroup; if Q-hat or K-hat
+    // reached 2^12, run the tile again with scaled logit operands.
+    {
+      const unsigned rq = wave_max_bits(amax_q), rk = wave_max_bits(amax_k);
+      if (lane == 0) sRange[wave] = u32x2{rq, rk};
+    }
+    lds_barrier();
+    unsigned rq = 0, rk = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const u32x2 r = sRange[w];
+      rq = max(rq, r[0]);
+      rk = max(rk, r[1]);
+    }
+    const unsigned eq = __builtin_amdgcn_readfirstlane(rq) >> 23;
+    const unsigned ek = __builtin_amdgcn_readfirstlane(rk) >> 23;
+    if (!rescaled && (eq >= kF16ExpLimit || ek >= kF16ExpLimit)) {
+      rescaled = true;
+      fq = f16_fit(eq);
+      fk = f16_fit(ek);
+      fsc = 1.f / (fq * fk);
+      amax_q = amax_k = 0.f;
+      continue;
     }
   }
 
@@ -392,6 +433,8 @@ bwd_dq_kernel(const BwdParams p) {
       }
     }
   }
+  break;
+  }   // pass
 }
 
 // ---------------------------------------------------------------------------
@@ -402,14 +445,18 @@ bwd_dq_kernel(const BwdParams p) {
 // computed, through buffer descriptors over the plane (rows >= N read 0), and
 // committed to LDS after the stage barrier.  Otherwise each stage is loaded
 // element-wise and synchronously.
-// PS (bf16 compute, head_dim >= 128): logits from split Q-hat (LDS, hi + lo)
-// and K-hat (registers, hi + lo), and dK-hat^T += Q-hat^T dS_hi + Q-hat^T dS_lo.
-template <typename IO, int CT, int D, int NW, int KT, int QS, bool VEC, bool PS>
+// FS (bf16 compute, head_dim >= 128): logits from fp16 operands (an fp16
+// Q-hat tile next to the bf16 one the dK product reads; K-hat in registers),
+// and dK-hat^T += Q-hat^T dS_hi + Q-hat^T dS_lo.  A tile whose Q-hat or K-hat
+// reaches 2^12 is computed again with scaled logit operands.
+template <typename IO, int CT, int D, int NW, int KT, int QS, bool VEC, bool FS>
 __global__ void __launch_bounds__(NW * 64)
 bwd_dkdv_kernel(const BwdParams p) {
   using C = Comp<CT>;
   using S = typename C::S;
   using Frag = typename C::Frag;
+  using LC = std::conditional_t<FS, Comp<DT_F16>, C>;   // logits operands
+  using LFrag = typename LC::Frag;
   constexpr int KS = D / 32, DT = D / 16, D2 = D / 2;
   constexpr int PADE = 16 / sizeof(S);
   constexpr int LDQ = D + PADE, LDT = QS + PADE;
@@ -420,9 +467,10 @@ bwd_dkdv_kernel(const BwdParams p) {
   // (ds_read_b64_tr_b16); fp32 storage keeps explicit transposed copies.
   constexpr bool TR = sizeof(S) == 2;
 
-  static_assert(!PS || CT == DT_BF16, "split operands are bf16");
+  static_assert(!FS || CT == DT_BF16, "fp16 logit operands go with bf16 compute");
   __shared__ __attribute__((aligned(16))) S sQ[QS * LDQ];
-  __shared__ __attribute__((aligned(16))) S sQl[PS ? QS * LDQ : 8];   // PS: Q-hat lo
+  __shared__ __attribute__((aligned(16))) f16 sQf[FS ? QS * LDQ : 8];   // FS: fp16 Q-hat (scaled)
+  __shared__ u32x2 sRange[FS ? NW : 1];   // FS: per-wave max |Q-hat|, |K-hat| bits
   __shared__ __attribute__((aligned(16))) S sQt[TR ? 8 : D * LDT];
   __shared__ __attribute__((aligned(16))) S sG[QS * LDQ];
   __shared__ __attribute__((aligned(16))) S sGt[TR ? 8 : D * LDT];
@@ -444,14 +492,24 @@ bwd_dkdv_kernel(const BwdParams p) {
   const int shift = 1 - p.has_cls;
   const int64_t prow = (int64_t)plane * N;
 
-  const int tid = thread_id();
+  // FS: largest |Q-hat| (scaled) and |K-hat| this thread converted in the
+  // current pass; the operand scales and the logit factor 1 / (fq fk) of a
+  // rescaled pass (all 1 otherwise)
+  float amax_q = 0.f, amax_k = 0.f;
+  float fq = 1.f, fk = 1.f, fsc = 1.f;
+  bool rescaled = false;
+  for (;;) {   // one pass, or two when FS rescales
+  // (FS: the lane index is opaque to the compiler, so that no lane-dependent
+  // address of the pass is hoisted out of this loop to hold registers)
+  const int tid = FS ? opaque(thread_id()) : thread_id();
   const int wave = tid >> 6, lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
   const int kv_first = kblk * KROWS + wave * KT * 16;
-
+  // LSE (natural log) -> the S accumulators' seed -LSE2 (FS: times fq fk)
+  const float l2seed = FS ? kLog2e * fq * fk : kLog2e;
   // ---- this wave's K-hat and V rows as B-operands ----
-  Frag kf[KT][KS], vf[KT][KS];
-  Frag kfl[PS ? KT : 1][PS ? KS : 1];   // PS: K-hat lo
+  LFrag kf[KT][KS];
+  Frag vf[KT][KS];
 #pragma unroll
   for (int u = 0; u < KT; ++u) {
     const int row = kv_first + 16 * u + lr;
@@ -465,20 +523,27 @@ bwd_dkdv_kernel(const BwdParams p) {
         rope_load4(tab, row + shift, D2, c0 / 2, cs);
         rope_rotate8(x, cs);
         // pre-scaled by softmax_scale * log2(e), as every kernel stages K-hat
+        // (fp16 operands: Q-hat carries the scale; K-hat times fk)
+        const float ks = FS ? fk : p.scale_log2;
+        if (!FS || rescaled) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] *= p.scale_log2;
+          for (int e = 0; e < 8; ++e) x[e] *= ks;
+        }
         load8(V + row * p.sv[2] + c0 * p.sv[3], p.sv[3], p.vec_v, y);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = y[e] = 0.f;
       }
-      if constexpr (PS)
-        split_bf16x8(x, kf[u][s].v, kfl[u][s].v);
-      else
+      if constexpr (FS) {
+        amax_k = amax8(amax_k, x);
+        kf[u][s].v = to_f16x8(x);
+      } else {
         kf[u][s] = C::make(x);
+      }
       vf[u][s] = C::make(y);
     }
   }
+  if constexpr (FS) amax_k = opaque(amax_k);
 
   f32x4 dvacc[KT][DT], dkacc[KT][DT];
 #pragma unroll
@@ -486,15 +551,16 @@ bwd_dkdv_kernel(const BwdParams p) {
 #pragma unroll
     for (int d = 0; d < DT; ++d) dvacc[u][d] = dkacc[u][d] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Q-hat row segment -> sQ (PS: hi to sQ, lo to sQl)
+  // Q-hat row segment -> sQ (FS: also Q-hat * scale * log2(e) * fq to sQf in fp16)
   auto put_qhat = [&](int off, const float (&xq)[8]) __attribute__((always_inline)) {
-    if constexpr (PS) {
-      bf16x8 hi, lo;
-      split_bf16x8(xq, hi, lo);
-      *reinterpret_cast<bf16x8*>(&sQ[off]) = hi;
-      *reinterpret_cast<bf16x8*>(&sQl[off]) = lo;
-    } else {
-      C::put8(&sQ[off], xq);
+    C::put8(&sQ[off], xq);
+    if constexpr (FS) {
+      const float qs = p.scale_log2 * fq;
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = xq[e] * qs;
+      amax_q = amax8(amax_q, x);
+      *reinterpret_cast<f16x8*>(&sQf[off]) = to_f16x8(x);
     }
   };
 
@@ -555,7 +621,7 @@ bwd_dkdv_kernel(const BwdParams p) {
         }
       }
       if (tid < QS) {   // negated: they seed the S and dP accumulators
-        sL2[tid] = qb + tid < N ? -pl * kLog2e : -INFINITY;
+        sL2[tid] = qb + tid < N ? -pl * l2seed : -INFINITY;
         sDl[tid] = qb + tid < N ? -pd : 0.f;
       }
     }
@@ -605,7 +671,7 @@ bwd_dkdv_kernel(const BwdParams p) {
       }
       for (int r = tid; r < rows; r += NT) {
         const int gr = qb + r;
-        sL2[r] = gr < N ? -p.lse[prow + gr] * kLog2e : -INFINITY;
+        sL2[r] = gr < N ? -p.lse[prow + gr] * l2seed : -INFINITY;
         sDl[r] = gr < N ? -p.delta[prow + gr] : 0.f;
       }
     }
@@ -630,14 +696,13 @@ bwd_dkdv_kernel(const BwdParams p) {
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             const int ql = 32 * j + 8 * (lr >> 2) + 4 * h + (lr & 3);
-            const Frag a = C::lds(&sQ[ql * LDQ + 32 * s + 8 * lg]);
+            LFrag a;
+            if constexpr (FS)
+              a = LC::lds(&sQf[ql * LDQ + 32 * s + 8 * lg]);
+            else
+              a = C::lds(&sQ[ql * LDQ + 32 * s + 8 * lg]);
             const Frag b = C::lds(&sG[ql * LDQ + 32 * s + 8 * lg]);
-            if constexpr (PS) {
-              const Frag al = C::lds(&sQl[ql * LDQ + 32 * s + 8 * lg]);
-              sacc[h] = C::mma(al, kf[u][s], sacc[h]);
-              sacc[h] = C::mma(a, kfl[u][s], sacc[h]);
-            }
-            sacc[h] = C::mma(a, kf[u][s], sacc[h]);
+            sacc[h] = LC::mma(a, kf[u][s], sacc[h]);
             pacc[h] = C::mma(b, vf[u][s], pacc[h]);
           }
         }
@@ -650,13 +715,14 @@ bwd_dkdv_kernel(const BwdParams p) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int e = 4 * h + i;
-            const float pr = fast_exp2(sacc[h][i]);
+            // FS: the seeds are -LSE2 * fq * fk, so this is exp2(S - LSE2)
+            const float pr = fast_exp2(FS ? sacc[h][i] * fsc : sacc[h][i]);
             pv[e] = pr;
             dsv[e] = pr * pacc[h][i];
           }
         const Frag pf = C::make(pv);
         Frag dsf, dsfl;
-        if constexpr (PS)
+        if constexpr (FS)
           split_bf16x8(dsv, dsf.v, dsfl.v);
         else
           dsf = C::make(dsv);
@@ -674,12 +740,39 @@ bwd_dkdv_kernel(const BwdParams p) {
             aq = C::lds(&sQt[(16 * d + lr) * LDT + 32 * j + 8 * lg]);
           }
           dvacc[u][d] = C::mma(ag, pf, dvacc[u][d]);
-          if constexpr (PS) dkacc[u][d] = C::mma(aq, dsfl, dkacc[u][d]);
+          if constexpr (FS) dkacc[u][d] = C::mma(aq, dsfl, dkacc[u][d]);
           dkacc[u][d] = C::mma(aq, dsf, dkacc[u][d]);
         }
       }
     }
 
+  }
+
+  if constexpr (FS) {
+    // Operand ranges of this pass over the workgroup; if Q-hat or K-hat
+    // reached 2^12, run the tile again with scaled logit operands.
+    {
+      const unsigned rq = wave_max_bits(amax_q), rk = wave_max_bits(amax_k);
+      if (lane == 0) sRange[wave] = u32x2{rq, rk};
+    }
+    lds_barrier();
+    unsigned rq = 0, rk = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const u32x2 r = sRange[w];
+      rq = max(rq, r[0]);
+      rk = max(rk, r[1]);
+    }
+    const unsigned eq = __builtin_amdgcn_readfirstlane(rq) >> 23;
+    const unsigned ek = __builtin_amdgcn_readfirstlane(rk) >> 23;
+    if (!rescaled && (eq >= kF16ExpLimit || ek >= kF16ExpLimit)) {
+      rescaled = true;
+      fq = f16_fit(eq);
+      fk = f16_fit(ek);
+      fsc = 1.f / (fq * fk);
+      amax_q = amax_k = 0.f;
+      continue;
+    }
   }
 
   // ---- epilogue: lane holds dV / dK-hat of kv row kv0 + lr, channels 16d + 4lg + (0..3) ----
@@ -698,6 +791,8 @@ bwd_dkdv_kernel(const BwdParams p) {
       }
     }
   }
+  break;
+  }   // pass
 }
 
 // ---------------------------------------------------------------------------
@@ -818,26 +913,26 @@ hipError_t launch_bwd_pre(const BwdParams& p, int io, int D, hipStream_t st) {
 template <typename IO, int CT, int D>
 static hipError_t dq_launch(const BwdParams& p0, bool write_delta, hipStream_t st) {
   using SH = BwdShape<D, CT == DT_F32>;
-  constexpr bool PS = precise_logits(CT, D);
+  constexpr bool FS = f16_logits(CT, D);
   BwdParams p = p0;
   const int grid = p.n_wg = p.B * p.H * p.n_blk;
   // (fp32 compute has no registers to spare for the prefetch)
   if constexpr (CT != DT_F32) {
     if (p.vec_k && p.vec_v) {
       if (write_delta)
-        hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, true, true, PS>),
+        hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, true, true, FS>),
                            dim3(grid), dim3(SH::DQ_NW * 64), 0, st, p);
       else
-        hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, false, true, PS>),
+        hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, false, true, FS>),
                            dim3(grid), dim3(SH::DQ_NW * 64), 0, st, p);
       return hipGetLastError();
     }
   }
   if (write_delta)
-    hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, true, false, PS>),
+    hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, true, false, FS>),
                        dim3(grid), dim3(SH::DQ_NW * 64), 0, st, p);
   else
-    hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, false, false, PS>),
+    hipLaunchKernelGGL((bwd_dq_kernel<IO, CT, D, SH::DQ_NW, SH::DQ_QT, SH::DQ_KVS, false, false, FS>),
                        dim3(grid), dim3(SH::DQ_NW * 64), 0, st, p);
   return hipGetLastError();
 }
@@ -845,18 +940,18 @@ static hipError_t dq_launch(const BwdParams& p0, bool write_delta, hipStream_t s
 template <typename IO, int CT, int D>
 static hipError_t dkdv_launch(const BwdParams& p0, hipStream_t st) {
   using SH = BwdShape<D, CT == DT_F32>;
-  constexpr bool PS = precise_logits(CT, D);
+  constexpr bool FS = f16_logits(CT, D);
   BwdParams p = p0;
   const int grid = p.n_wg = p.B * p.H * p.n_blk;
   // (fp32 compute has no registers to spare for the prefetch)
   if constexpr (CT != DT_F32) {
     if (p.vec_q && p.vec_do) {
-      hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS, true, PS>), dim3(grid),
+      hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS, true, FS>), dim3(grid),
                          dim3(SH::KV_NW * 64), 0, st, p);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS, false, PS>), dim3(grid),
+  hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS, false, FS>), dim3(grid),
                      dim3(SH::KV_NW * 64), 0, st, p);
   return hipGetLastError();
 }

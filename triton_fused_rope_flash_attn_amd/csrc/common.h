@@ -387,7 +387,7 @@ template <> struct Comp<DT_F32> {
 };
 
 // ---------------------------------------------------------------------------
-// Split bf16 operands (bf16 compute, "precise" products): x = hi + lo with
+// Split bf16 operands (dS at bf16 compute, head_dim >= 128): x = hi + lo with
 // hi = bf16(x) and lo = bf16(x - hi), about 16 significant bits between them.
 // A product a.b is then taken as a_hi.b_hi + a_lo.b_hi + a_hi.b_lo (the
 // dropped a_lo.b_lo is below the fp32 accumulation error); with one operand
@@ -410,6 +410,48 @@ __device__ __forceinline__ void split_bf16x8(const float (&x)[8], bf16x8& hi, bf
     lo[2 * p] = l[0];
     lo[2 * p + 1] = l[1];
   }
+}
+
+// ---------------------------------------------------------------------------
+// fp16 logit operands (bf16 compute at head_dim >= 128): the rotated Q / K
+// rows enter the logits product rounded to fp16 (11 significant bits against
+// bf16's 8), one MFMA per product.  fp16 ends at 65504 and has normal values
+// down to 2^-14 only, so each kernel keeps the largest |x| it converts.  When
+// a tile's Q-hat or K-hat reaches 2^12 -- past that fp16 could overflow, or
+// the other operand's values in fp16's subnormal range could shift a logit by
+// more than 128 * 2^-25 * 2^12 = 2^-6 -- the tile is computed once more with
+// both operands scaled by f16_fit (powers of two that put each maximum in
+// [2^14, 2^15)) and the logits multiplied by the inverse scales in fp32.
+// Otherwise the scales are 1 and the factor is exact.
+// ---------------------------------------------------------------------------
+constexpr unsigned kF16ExpLimit = 139;   // biased fp32 exponent of 2^12
+
+// running max of |x| over 8 values (NaN is ignored)
+__device__ __forceinline__ float amax8(float a, const float (&x)[8]) {
+#pragma unroll
+  for (int p = 0; p < 4; ++p) a = fmaxf(a, fmaxf(fabsf(x[2 * p]), fabsf(x[2 * p + 1])));
+  return a;
+}
+// fp16 images of 8 values, two per packed conversion (round to nearest even)
+__device__ __forceinline__ f16x8 to_f16x8(const float (&x)[8]) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef f16 h2 __attribute__((ext_vector_type(2)));
+  f16x8 r;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const h2 h = __builtin_convertvector(f2{x[2 * p], x[2 * p + 1]}, h2);
+    r[2 * p] = h[0];
+    r[2 * p + 1] = h[1];
+  }
+  return r;
+}
+// Operand scale of a rescaled pass for a maximum |x| with biased exponent e:
+// 2^(141 - e), which puts the scaled maximum in [2^14, 2^15), at most 2^64
+// (an operand that small contributes nothing a logit could resolve).
+// e = 255 (inf) gives 2^-114, which leaves inf as inf: such inputs end as
+// inf / NaN, as they do in fp32 arithmetic.
+__device__ __forceinline__ float f16_fit(unsigned e) {
+  return __uint_as_float((e >= 77u ? 268u - e : 191u) << 23);
 }
 
 // ---------------------------------------------------------------------------
@@ -442,6 +484,19 @@ __device__ __forceinline__ float xor32_pair_op_max(float v) {
 }
 __device__ __forceinline__ float group4_sum(float v) { return xor32_pair_op_sum(xor16_pair_op_sum(v)); }
 __device__ __forceinline__ float group4_max(float v) { return xor32_pair_op_max(xor16_pair_op_max(v)); }
+
+// Largest of a non-negative float over the wave, as its fp32 bit pattern
+// (those order like the values), in every lane: DPP within each 16-lane row
+// (both quad permutations, then the mirror images within the half row and
+// the row), then the two row swaps.  (No __shfl: those are device-library
+// calls that these kernels, built with IEEE mode off, would not inline.)
+__device__ __forceinline__ unsigned wave_max_bits(float x) {
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false)));
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false)));
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false)));
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xF, 0xF, false)));
+  return __float_as_uint(group4_max(x));
+}
 
 // Work-item / workgroup ids straight from the hardware registers.  (The
 // threadIdx / blockIdx / gridDim accessors are device-library calls, and the
@@ -503,6 +558,13 @@ __device__ __forceinline__ float dpp_sum8(float x) {
 // loops, which keeps per-lane addresses of rarely run phases (per-plane
 // prologue / epilogue) from occupying registers through the hot loop.
 __device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+// The same for a float: pins a value computed early (a running maximum of
+// converted operands) where it is computed, instead of letting its inputs
+// stay live until the value's only use at the end of a tile.
+__device__ __forceinline__ float opaque(float x) {
   asm volatile("" : "+v"(x));
   return x;
 }

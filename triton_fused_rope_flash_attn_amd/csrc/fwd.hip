@@ -79,16 +79,19 @@ constexpr float kRescaleSlack = 8.0f;   // log2 units: P <= 2^8 between rescales
 
 // VEC: every tensor of the call allows 16-byte vector access (decided on the
 // host); the generic instantiation gathers element by element instead.
-// PS (bf16 compute): the logits are taken from split operands, K-hat = hi + lo
-// (two LDS tiles) and Q-hat = hi + lo (registers), as hi.hi + lo.hi + hi.lo:
-// the rounding of the rotated rows to bf16 is what dominates the error of
-// bf16 attention at long, wide planes, and it no longer enters S.
-template <typename IO, int CT, int D, int NW, int QT, int KC, int TABROWS, bool VEC, bool PS>
+// FS (bf16 compute): the logits product takes fp16 operands (K-hat tile in
+// LDS, Q-hat fragments in registers): the rounding of the rotated rows to
+// bf16 is what dominates the error of bf16 attention at long, wide planes.
+// P and V stay bf16.  An item whose Q-hat or K-hat reaches 2^12 is computed
+// again with scaled operands (f16_fit in common.h).
+template <typename IO, int CT, int D, int NW, int QT, int KC, int TABROWS, bool VEC, bool FS>
 __global__ void __launch_bounds__(NW * 64)
 fwd_kernel(const FwdParams p) {
   using C = Comp<CT>;
   using S = typename C::S;
   using Frag = typename C::Frag;
+  using LC = std::conditional_t<FS, Comp<DT_F16>, C>;   // logits operands
+  using LFrag = typename LC::Frag;
   constexpr int KS = D / 32;          // k-steps of 32 channels
   constexpr int DT = D / 16;          // 16-channel output subtiles
   constexpr int D2 = D / 2;
@@ -112,9 +115,10 @@ fwd_kernel(const FwdParams p) {
   // row-major and each V^T fragment is gathered element by element (VROW).
   constexpr bool TRV = sizeof(S) == 2;
   constexpr bool VROW = !TRV && D >= 256;
-  static_assert(!PS || CT == DT_BF16, "split operands are bf16");
-  __shared__ __attribute__((aligned(16))) S sK[2][KC * LDK];
-  __shared__ __attribute__((aligned(16))) S sKl[2][PS ? KC * LDK : 8];   // PS: K-hat lo
+  static_assert(!FS || CT == DT_BF16, "fp16 logit operands go with bf16 compute");
+  __shared__ __attribute__((aligned(16))) S sK[2][KC * LDK];   // FS: fp16 K-hat
+  // FS: per-wave max |Q-hat|, max |K-hat| bit patterns of an item pass
+  __shared__ u32x2 sRange[FS ? NW : 1];
   __shared__ __attribute__((aligned(16))) S sVt[2][(TRV || VROW) ? KC * LDK : D * LDV];
   // LDS copy of the packed table: D/2 (cos, sin) pairs = D floats per row,
   // 16-byte chunk c of row r stored at chunk c ^ (r & (D/4 - 1)) (bank-spread
@@ -175,6 +179,14 @@ fwd_kernel(const FwdParams p) {
   auto rsrc = [&](const void* b, const int64_t* st, int plane) __attribute__((always_inline)) {
     return make_rsrc(plane_base(b, st, plane), (unsigned)(((int64_t)(N - 1) * st[2] + D) * ES));
   };
+
+  // FS: largest |Q-hat| (scaled) and |K-hat| this thread converted in the
+  // current pass of an item; the operand scales and the logit factor
+  // 1 / (fq fk) of a rescaled pass (all 1 otherwise).
+  float amax_q = 0.f, amax_k = 0.f;
+  float fq = 1.f, fk = 1.f, fsc = 1.f;
+  bool rescaled = false, redo = false;
+  unsigned eq = 0, ek = 0;   // biased exponents of the pass's max |Q-hat|, |K-hat|
 
   // ---- KV chunk prefetch registers: two rows x 8 channels of K and V
   //      (+ their cos/sin when the table is not in LDS) ----
@@ -282,17 +294,19 @@ fwd_kernel(const FwdParams p) {
           // K-hat pre-scaled by softmax_scale * log2(e): the logits come out
           // of the MFMAs in log2 units (every kernel stages K-hat this way, so
           // the forward and backward passes see bit-identical logits).  With
-          // split operands Q-hat carries the scale instead: it is staged once
-          // per item, K-hat once per chunk.
-          if constexpr (!PS) {
+          // fp16 operands Q-hat carries the scale instead (in every kernel):
+          // it is staged once per item, K-hat once per chunk.
+          if constexpr (!FS) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) xk[e] *= c2;
           }
-          if constexpr (PS) {
-            bf16x8 hi, lo;
-            split_bf16x8(xk, hi, lo);
-            *reinterpret_cast<bf16x8*>(&sK[slot][kperm(2 * rp + x) * LDK + 8 * cc]) = hi;
-            *reinterpret_cast<bf16x8*>(&sKl[slot][kperm(2 * rp + x) * LDK + 8 * cc]) = lo;
+          if constexpr (FS) {
+            if (rescaled) {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) xk[e] *= fk;
+            }
+            amax_k = amax8(amax_k, xk);
+            *reinterpret_cast<f16x8*>(&sK[slot][kperm(2 * rp + x) * LDK + 8 * cc]) = to_f16x8(xk);
           } else {
             C::put8(&sK[slot][kperm(2 * rp + x) * LDK + 8 * cc], xk);
           }
@@ -319,11 +333,12 @@ fwd_kernel(const FwdParams p) {
   };
 
   // ---- Q rows of an item: raw prefetch registers -> rotated B-operand fragments ----
-  // At D = 128 with two subtiles per wave, or with split operands and 32-bit
-  // tensors, the rows load when the item starts instead: the prefetch
-  // registers (rows and table values) would not fit beside the Q-hat
-  // fragments and O accumulators.
-  constexpr bool kQpf = !(D == 128 && (QT > 1 || (PS && sizeof(IO) == 4)));
+  // At D = 128 with two subtiles per wave, or with fp16 logit operands, the
+  // rows load when the item starts instead: the prefetch registers (rows and
+  // table values) would not fit beside the Q-hat fragments and O
+  // accumulators, and an item computed again (fp16 operand range) needs its
+  // own rows.
+  constexpr bool kQpf = !(FS || (D == 128 && QT > 1));
   Raw8<IO> qraw[kQpf ? QT : 1][kQpf ? KS : 1];
   float qcs[kQpf ? QT : 1][kQpf ? KS : 1][kTabLds ? 1 : 8];
   auto prefetch_q = [&](int item) __attribute__((always_inline)) {
@@ -360,8 +375,7 @@ fwd_kernel(const FwdParams p) {
       }
     }
   };
-  Frag qf[QT][KS];
-  Frag qfl[PS ? QT : 1][PS ? KS : 1];   // PS: Q-hat lo
+  LFrag qf[QT][KS];
   auto commit_q = [&](int plane, int qb) __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < QT; ++t)
@@ -391,10 +405,12 @@ fwd_kernel(const FwdParams p) {
           rope_rotate8(x, qcs[t][s]);
         }
         }
-        if constexpr (PS) {
+        if constexpr (FS) {
+          const float qs = c2 * fq;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] *= c2;
-          split_bf16x8(x, qf[t][s].v, qfl[t][s].v);
+          for (int e = 0; e < 8; ++e) x[e] *= qs;
+          amax_q = amax8(amax_q, x);
+          qf[t][s].v = to_f16x8(x);
         } else {
           qf[t][s] = C::make(x);
         }
@@ -448,12 +464,14 @@ fwd_kernel(const FwdParams p) {
   auto logits = [&](const KFr& kf, SAcc& sa) __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < QT; ++t) sa[t][0] = sa[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (!FS) {   // (the pipelined chunk runs without fp16 operands)
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
+      for (int s = 0; s < KS; ++s)
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int t = 0; t < QT; ++t) sa[t][h] = C::mma(kf[s][h], qf[t][s], sa[t][h]);
+          for (int t = 0; t < QT; ++t) sa[t][h] = C::mma(kf[s][h], qf[t][s], sa[t][h]);
+    }
   };
   // Online softmax of one block; the lane holds keys 8lg + (0..7) of the
   // block for its query row.  MASKED: keys e >= lim get probability 0.
@@ -587,7 +605,7 @@ fwd_kernel(const FwdParams p) {
   // Without the LDS table (D = 128 or long planes), or with 32-bit I/O (twice
   // the prefetch registers), the registers of the pipeline are not free: the
   // same work block by block.
-  constexpr bool kPipe = kTabLds && sizeof(IO) == 2 && !PS;
+  constexpr bool kPipe = kTabLds && sizeof(IO) == 2 && !FS;
   // One KV chunk for all QT subtiles of the wave.  Subtiles past the last
   // query row hold zero rows and are computed anyway: every wave of a
   // workgroup then runs the same instruction stream with no per-subtile
@@ -599,8 +617,7 @@ fwd_kernel(const FwdParams p) {
   // last query row hold zero rows and are computed anyway: every wave of a
   // workgroup then runs the same instruction stream with no per-subtile
   // guards.  MASKED: the block holding key N-1 (keys >= N get probability 0).
-  auto blk_logits = [&](const S* __restrict__ cK, const S* __restrict__ cKl, int j, SAcc& sacc)
-      __attribute__((always_inline)) {
+  auto blk_logits = [&](const S* __restrict__ cK, int j, SAcc& sacc) __attribute__((always_inline)) {
     // ---- S^T = K-hat Q-hat^T for 32 keys (each K-hat fragment feeds QT MFMAs) ----
 #pragma unroll
     for (int t = 0; t < QT; ++t) sacc[t][0] = sacc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -609,17 +626,9 @@ fwd_kernel(const FwdParams p) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int off = (32 * j + 16 * h + lr) * LDK + 32 * s + 8 * lg;
-        const Frag a = C::lds(&cK[off]);
-        if constexpr (PS) {
-          const Frag al = C::lds(&cKl[off]);
+        const LFrag a = LC::lds(reinterpret_cast<const typename LC::S*>(&cK[off]));
 #pragma unroll
-          for (int t = 0; t < QT; ++t) {
-            sacc[t][h] = C::mma(al, qf[t][s], sacc[t][h]);
-            sacc[t][h] = C::mma(a, qfl[t][s], sacc[t][h]);
-          }
-        }
-#pragma unroll
-        for (int t = 0; t < QT; ++t) sacc[t][h] = C::mma(a, qf[t][s], sacc[t][h]);
+        for (int t = 0; t < QT; ++t) sacc[t][h] = LC::mma(a, qf[t][s], sacc[t][h]);
       }
     }
   };
@@ -642,9 +651,12 @@ fwd_kernel(const FwdParams p) {
       }
       // The running max only has to bound the exponent: rescale (group max,
       // O and row sum times 2^(m_old - m_new)) only when some lane's own max
-      // exceeds m_thr = m_run + slack (log2 units).
-      const float ml = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                             fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+      // exceeds m_thr = m_run + slack (log2 units).  FS: the logits are
+      // fsc * sv (fsc = 1 except in a rescaled pass), folded into the max
+      // and into the exponent's subtraction.
+      float ml = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                       fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+      if constexpr (FS) ml *= fsc;
       if (__any(ml > m_thr[t])) {
         const float mx = group4_max(ml);
         const float mnew = fmaxf(m_run[t], mx);
@@ -658,7 +670,7 @@ fwd_kernel(const FwdParams p) {
       float pv8[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        pv8[e] = fast_exp2(sv[e] - m_run[t]);
+        pv8[e] = fast_exp2(FS ? __builtin_fmaf(sv[e], fsc, -m_run[t]) : sv[e] - m_run[t]);
         l_run[t] += pv8[e];
       }
       pf[t] = C::make(pv8);
@@ -680,12 +692,11 @@ fwd_kernel(const FwdParams p) {
   };
   // One KV chunk of nb blocks (the last one ragged when N - kvb < KC and not
   // a multiple of 32).  With one subtile per wave the logits of block j+1 are
-  // issued before the softmax of block j, so that those MFMAs (three per
-  // product with split operands) run while the VALU computes block j's
+  // issued before the softmax of block j, so that those MFMAs run while the
+  // VALU computes block j's
   // probabilities; two blocks per trip alternate the two logit accumulators
   // without copies.
-  auto chunk_serial = [&](const S* __restrict__ cK, const S* __restrict__ cKl, const S* __restrict__ cV,
-                          int kvb) __attribute__((always_inline)) {
+  auto chunk_serial = [&](const S* __restrict__ cK, const S* __restrict__ cV, int kvb) __attribute__((always_inline)) {
     const int nkeys = min(KC, N - kvb);
     if constexpr (QT == 1 && sizeof(S) == 2) {
       // every block goes through the masked softmax (a key limit past the
@@ -693,12 +704,12 @@ fwd_kernel(const FwdParams p) {
       // pipelined loop within the register budget
       const int nb = (nkeys + 31) >> 5;
       SAcc sA, sB;
-      blk_logits(cK, cKl, 0, sA);
+      blk_logits(cK, 0, sA);
       int j = 0;
       for (; j + 1 < nb; j += 2) {
-        blk_logits(cK, cKl, j + 1, sB);
+        blk_logits(cK, j + 1, sB);
         blk_out(std::true_type{}, cV, kvb, j, sA);
-        if (j + 2 < nb) blk_logits(cK, cKl, j + 2, sA);
+        if (j + 2 < nb) blk_logits(cK, j + 2, sA);
         blk_out(std::true_type{}, cV, kvb, j + 1, sB);
       }
       if (j < nb) blk_out(std::true_type{}, cV, kvb, j, sA);   // odd block count: last logits in sA
@@ -708,11 +719,11 @@ fwd_kernel(const FwdParams p) {
       const int nfull = nkeys / 32;
       SAcc sA;
       for (int j = 0; j < nfull; ++j) {
-        blk_logits(cK, cKl, j, sA);
+        blk_logits(cK, j, sA);
         blk_out(std::false_type{}, cV, kvb, j, sA);
       }
       if (nkeys % 32) {
-        blk_logits(cK, cKl, nfull, sA);
+        blk_logits(cK, nfull, sA);
         blk_out(std::true_type{}, cV, kvb, nfull, sA);
       }
     }
@@ -751,7 +762,7 @@ fwd_kernel(const FwdParams p) {
   // RES: O's rounding residual bf16(O - bf16(O)) goes to p.o_res (contiguous
   // [B, H, N, D]) next to O, for the backward's delta; stored only when the
   // caller gave the buffer (a uniform test)
-  constexpr bool RES = PS && std::is_same<IO, bf16>::value;
+  constexpr bool RES = FS && std::is_same<IO, bf16>::value;
   u32x2 ostr[kDefer && RES ? QT : 1][DT];
   auto res4 = [](const float (&o4)[4], const IO (&h4)[4], float (&r4)[4]) __attribute__((always_inline)) {
 #pragma unroll
@@ -830,6 +841,31 @@ fwd_kernel(const FwdParams p) {
       constexpr bool FIRST = decltype(firstc)::value;
       const int slot = g & 1;
       commit_kv(slot, chunk_start(c));
+      if constexpr (FS) {
+        // After the item's last K-hat chunk is converted: the operand ranges
+        // of this pass over the workgroup (each wave's, through LDS, read
+        // between this barrier and the next; the next pass writes after
+        // both).  If Q-hat or K-hat reached 2^12, the item is computed again
+        // with scaled operands, and the prefetch below loads its first chunk
+        // once more.
+        if (c == nch - 1) {
+          {
+            const unsigned rq = wave_max_bits(amax_q), rk = wave_max_bits(amax_k);
+            if (lane == 0) sRange[wave] = u32x2{rq, rk};
+          }
+          lds_barrier();
+          unsigned rq = 0, rk = 0;
+#pragma unroll
+          for (int w = 0; w < NW; ++w) {
+            const u32x2 r = sRange[w];
+            rq = max(rq, r[0]);
+            rk = max(rk, r[1]);
+          }
+          eq = __builtin_amdgcn_readfirstlane(rq) >> 23;
+          ek = __builtin_amdgcn_readfirstlane(rk) >> 23;
+          redo = !rescaled && (eq >= kF16ExpLimit || ek >= kF16ExpLimit);
+        }
+      }
       if constexpr (FIRST && kPipe) flush_o();
       auto mem = [&]() __attribute__((always_inline)) {
         if constexpr (FIRST) {
@@ -840,7 +876,7 @@ fwd_kernel(const FwdParams p) {
           prefetch_q(nxt >= 0 ? nxt : item);
         }
         const bool last = c + 1 == nch;
-        const int tgt = last ? (nxt >= 0 ? nxt : item) : item;
+        const int tgt = last && !redo ? (nxt >= 0 ? nxt : item) : item;
         if (last) kvr = kv_rs(tgt);
         prefetch_kv(tgt, kvr, last ? 0 : c + 1);
       };
@@ -857,12 +893,28 @@ fwd_kernel(const FwdParams p) {
       } else {
         mem();
         lds_barrier();
-        if (nt > 0) chunk_serial(sK[slot], sKl[PS ? slot : 0], sVt[slot], chunk_start(c));
+        if (nt > 0) chunk_serial(sK[slot], sVt[slot], chunk_start(c));
       }
       ++g;
     };
     chunk_step(std::true_type{}, 0);
     for (int c = 1; c < nch; ++c) chunk_step(std::false_type{}, c);
+
+    if constexpr (FS) {
+      // a rescaled second pass (its first chunk is already on the way; no
+      // Q prefetch or deferred store exists with these operands); no store
+      amax_q = amax_k = 0.f;
+      if (redo) {
+        redo = false;
+        rescaled = true;
+        fq = f16_fit(eq);
+        fk = f16_fit(ek);
+        fsc = 1.f / (fq * fk);
+        continue;
+      }
+      rescaled = false;
+      fq = fk = fsc = 1.f;
+    }
 
     // ---- epilogue: lane holds O[row][16d + 4lg + (0..3)] ----
     if constexpr (kDefer) {
@@ -978,8 +1030,8 @@ template <> struct FwdShape<128> { static constexpr int NW = 8, QT = 1, KC = 64,
 template <> struct FwdShape<256> { static constexpr int NW = 4, QT = 1, KC = 32, TABROWS = 0; };
 
 // Query subtiles per wave at D = 128: two with 16-bit tensors and 16-bit
-// compute, so that every staged K-hat chunk (rotated, and split with
-// split-operand logits, once per item) serves twice the queries; their Q rows
+// compute, so that every staged K-hat chunk (rotated and converted once per
+// item) serves twice the queries; their Q rows
 // then load at the item start (no prefetch).  32-bit tensors or compute need
 // those registers for staging.
 template <int D, int CT, bool IO16> constexpr int fwd_qt() {
@@ -1006,16 +1058,16 @@ static hipError_t fwd_launch(const FwdParams& p0, hipStream_t st) {
   FwdParams p = p0;
   // fp32 compute keeps 4-byte tiles in LDS: no room for the table copy there
   constexpr int TR = CT == DT_F32 ? 0 : SH::TABROWS;
-  // split-operand logits for bf16 compute at head_dim >= 128 (the backward's
+  // fp16 logit operands for bf16 compute at head_dim >= 128 (the backward's
   // split kernels use the same rule, so both passes see the same S)
-  constexpr bool PS = precise_logits(CT, D);
+  constexpr bool FS = f16_logits(CT, D);
   constexpr int QT = fwd_qt<D, CT, sizeof(IO) == 2>();
   const bool tab = TR > 0 && p.N + 1 - p.has_cls <= TR;
   const bool vec = p.vec_q && p.vec_k && p.vec_v && p.vec_o;
-  auto kern = tab ? (vec ? fwd_kernel<IO, CT, D, SH::NW, QT, SH::KC, TR, true, PS>
-                         : fwd_kernel<IO, CT, D, SH::NW, QT, SH::KC, TR, false, PS>)
-                  : (vec ? fwd_kernel<IO, CT, D, SH::NW, QT, SH::KC, 0, true, PS>
-                         : fwd_kernel<IO, CT, D, SH::NW, QT, SH::KC, 0, false, PS>);
+  auto kern = tab ? (vec ? fwd_kernel<IO, CT, D, SH::NW, QT, SH::KC, TR, true, FS>
+                         : fwd_kernel<IO, CT, D, SH::NW, QT, SH::KC, TR, false, FS>)
+                  : (vec ? fwd_kernel<IO, CT, D, SH::NW, QT, SH::KC, 0, true, FS>
+                         : fwd_kernel<IO, CT, D, SH::NW, QT, SH::KC, 0, false, FS>);
   const int grid = persistent_grid(reinterpret_cast<const void*>(kern), SH::NW * 64, p.n_items);
   if (grid <= 0) return hipErrorInvalidConfiguration;
   p.n_wg = grid;

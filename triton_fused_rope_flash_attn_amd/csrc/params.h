@@ -14,7 +14,7 @@ struct FwdParams {
   const void* k;
   const void* v;
   void* o;
-  void* o_res;         // optional contiguous [B, H, N, D]: bf16(O - bf16(O)) (see precise_logits)
+  void* o_res;         // optional contiguous [B, H, N, D]: bf16(O - bf16(O)) (see o_residual)
   float* lse;          // [B*H, N] fp32, natural-log log-sum-exp of the logits
   int64_t sq[4], sk[4], sv[4], so[4];
   const float* rope;   // packed (cos, sin) table [(n_pos + 1), D/2, 2]
@@ -77,17 +77,20 @@ hipError_t launch_bwd_tail_rows(const BwdParams& p, int io, int D, int row0, boo
                                 hipStream_t st);
 hipError_t launch_bwd_tail_keys(const BwdParams& p, int io, int D, int key0, hipStream_t st);
 
-// Split-operand ("precise") logits and dS: bf16 compute at head_dim >= 128.
+// fp16 logit operands and split dS: bf16 compute at head_dim >= 128.
 // Rounding the rotated Q / K rows to bf16 before the logits product is the
 // dominant error of bf16 attention there (long, wide planes with large
-// logits); fp16 compute keeps 3 more mantissa bits and fp32 compute splits
+// logits).  Those kernels round them to fp16 instead (3 more mantissa bits;
+// operands beyond fp16's range are handled by a rescaled second pass, see
+// f16_fit in common.h) and take the dQ / dK products from dS = hi + lo (two
+// bf16 parts).  fp16 compute is fp16 throughout, and fp32 compute splits
 // every operand anyway.
-constexpr bool precise_logits(int ct, int D) { return ct == 2 /* DT_BF16 */ && D >= 128; }
-// With split-operand logits the remaining dQ / dK error is delta = rowsum(dO * O)
+constexpr bool f16_logits(int ct, int D) { return ct == 2 /* DT_BF16 */ && D >= 128; }
+// With those logits the next dQ / dK error term is delta = rowsum(dO * O)
 // taken from the bf16-stored O.  bf16 I/O then also stores O's rounding
 // residual bf16(O - bf16(O)) (when the caller provides the buffer), and the
 // backward takes delta from O + residual.
-constexpr bool o_residual(int io, int ct, int D) { return io == 2 && precise_logits(ct, D); }
+constexpr bool o_residual(int io, int ct, int D) { return io == 2 && f16_logits(ct, D); }
 
 // Workgroups for a persistent kernel: min(items, CUs x resident workgroups per
 // CU), with `dyn_lds` bytes of dynamic LDS per workgroup; <= 0 on a HIP error.
