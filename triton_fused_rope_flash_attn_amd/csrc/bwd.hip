@@ -215,7 +215,7 @@ bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) xk[e] *= fk;
       }
-      amax_k = amax8(amax_k, xk);
+      amax_k = opaque(amax8(amax_k, xk));   // (computed here, not at the tile's end)
       *reinterpret_cast<f16x8*>(&sKf[off]) = to_f16x8(xk);
     }
   };
@@ -559,7 +559,7 @@ bwd_dkdv_kernel(const BwdParams p) {
       float x[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) x[e] = xq[e] * qs;
-      amax_q = amax8(amax_q, x);
+      amax_q = opaque(amax8(amax_q, x));   // (computed here, not at the tile's end)
       *reinterpret_cast<f16x8*>(&sQf[off]) = to_f16x8(x);
     }
   };
@@ -678,19 +678,15 @@ bwd_dkdv_kernel(const BwdParams p) {
     lds_barrier();
     }
 
-    for (int j = 0; j < rows / 32; ++j) {
-      // -LSE2 and -delta of queries 32j + 8lg + e, e = 4h + i: the S and dP
-      // accumulator seeds of half h (P = exp2(S), dP - delta need no
-      // arithmetic; queries >= N have -LSE2 = -inf, so P = 0)
-      const f32x4 nl2[2] = {*reinterpret_cast<const f32x4*>(&sL2[32 * j + 8 * lg]),
-                            *reinterpret_cast<const f32x4*>(&sL2[32 * j + 8 * lg + 4])};
-      const f32x4 ndl[2] = {*reinterpret_cast<const f32x4*>(&sDl[32 * j + 8 * lg]),
-                            *reinterpret_cast<const f32x4*>(&sDl[32 * j + 8 * lg + 4])};
-#pragma unroll
-      for (int u = 0; u < KT; ++u) {
-        const int kv0 = kv_first + 16 * u;
-        if (kv0 >= N) continue;   // wave-uniform
-        f32x4 sacc[2] = {nl2[0], nl2[1]}, pacc[2] = {ndl[0], ndl[1]};
+    // S and dP of query block j for key subtile u.  -LSE2 and -delta of
+    // queries 32j + 8lg + e, e = 4h + i, seed the accumulators of half h
+    // (P = exp2(S), dP - delta need no arithmetic; queries >= N have
+    // -LSE2 = -inf, so P = 0).
+    auto sp = [&](int j, int u, f32x4 (&sacc)[2], f32x4 (&pacc)[2]) __attribute__((always_inline)) {
+        sacc[0] = *reinterpret_cast<const f32x4*>(&sL2[32 * j + 8 * lg]);
+        sacc[1] = *reinterpret_cast<const f32x4*>(&sL2[32 * j + 8 * lg + 4]);
+        pacc[0] = *reinterpret_cast<const f32x4*>(&sDl[32 * j + 8 * lg]);
+        pacc[1] = *reinterpret_cast<const f32x4*>(&sDl[32 * j + 8 * lg + 4]);
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
 #pragma unroll
@@ -706,6 +702,10 @@ bwd_dkdv_kernel(const BwdParams p) {
             pacc[h] = C::mma(b, vf[u][s], pacc[h]);
           }
         }
+    };
+    // P and dS of query block j from its S / dP, then dV += P dO and
+    // dK-hat += dS Q-hat for key subtile u.
+    auto pdk = [&](int j, int u, const f32x4 (&sacc)[2], const f32x4 (&pacc)[2]) __attribute__((always_inline)) {
         // Keys >= N (lane key kv0 + lr) need no mask: their K-hat and V rows
         // are zero, so P and dS there are finite and only reach the dK / dV
         // rows of those keys, which are never stored.
@@ -743,9 +743,33 @@ bwd_dkdv_kernel(const BwdParams p) {
           if constexpr (FS) dkacc[u][d] = C::mma(aq, dsfl, dkacc[u][d]);
           dkacc[u][d] = C::mma(aq, dsf, dkacc[u][d]);
         }
+    };
+
+    if constexpr (KT == 1 && sizeof(S) == 2) {
+      // Two query blocks per trip: the S / dP products of block j+1 go to the
+      // MFMA pipe before block j's probabilities are computed on the VALU (a
+      // ragged last block recomputes block j instead and skips its update).
+      if (kv_first < N) {   // wave-uniform
+        const int nbj = rows / 32;
+        for (int j = 0; j < nbj; j += 2) {
+          f32x4 sA[2], pA[2], sB[2], pB[2];
+          sp(j, 0, sA, pA);
+          sp(min(j + 1, nbj - 1), 0, sB, pB);
+          pdk(j, 0, sA, pA);
+          if (j + 1 < nbj) pdk(j + 1, 0, sB, pB);
+        }
+      }
+    } else {
+      for (int j = 0; j < rows / 32; ++j) {
+#pragma unroll
+        for (int u = 0; u < KT; ++u) {
+          if (kv_first + 16 * u >= N) continue;   // wave-uniform
+          f32x4 sacc[2], pacc[2];
+          sp(j, u, sacc, pacc);
+          pdk(j, u, sacc, pacc);
+        }
       }
     }
-
   }
 
   if constexpr (FS) {

@@ -305,7 +305,7 @@ fwd_kernel(const FwdParams p) {
 #pragma unroll
               for (int e = 0; e < 8; ++e) xk[e] *= fk;
             }
-            amax_k = amax8(amax_k, xk);
+            amax_k = opaque(amax8(amax_k, xk));   // (computed here, not at the item's end)
             *reinterpret_cast<f16x8*>(&sK[slot][kperm(2 * rp + x) * LDK + 8 * cc]) = to_f16x8(xk);
           } else {
             C::put8(&sK[slot][kperm(2 * rp + x) * LDK + 8 * cc], xk);
@@ -691,14 +691,14 @@ fwd_kernel(const FwdParams p) {
     }
   };
   // One KV chunk of nb blocks (the last one ragged when N - kvb < KC and not
-  // a multiple of 32).  With one subtile per wave the logits of block j+1 are
-  // issued before the softmax of block j, so that those MFMAs run while the
-  // VALU computes block j's
-  // probabilities; two blocks per trip alternate the two logit accumulators
-  // without copies.
+  // a multiple of 32).  With one subtile per wave, or two at D >= 128 with
+  // 16-bit operands and vector access, the logits of block j+1 are issued
+  // before the softmax of block j, so that those MFMAs run while the VALU
+  // computes block j's probabilities; two blocks per trip alternate the two
+  // logit accumulators without copies.
   auto chunk_serial = [&](const S* __restrict__ cK, const S* __restrict__ cV, int kvb) __attribute__((always_inline)) {
     const int nkeys = min(KC, N - kvb);
-    if constexpr (QT == 1 && sizeof(S) == 2) {
+    if constexpr (sizeof(S) == 2 && (QT == 1 || (VEC && D >= 128))) {
       // every block goes through the masked softmax (a key limit past the
       // block for full ones): one inlined copy per call site keeps the
       // pipelined loop within the register budget
@@ -714,8 +714,9 @@ fwd_kernel(const FwdParams p) {
       }
       if (j < nb) blk_out(std::true_type{}, cV, kvb, j, sA);   // odd block count: last logits in sA
     } else {
-      // two subtiles per wave, or fp32 compute (split operands): two blocks'
-      // logits do not fit beside their accumulators, so block by block
+      // two subtiles per wave at D <= 64 or with element-wise access, or fp32
+      // compute (split operands): two blocks' logits do not fit beside their
+      // accumulators, so block by block
       const int nfull = nkeys / 32;
       SAcc sA;
       for (int j = 0; j < nfull; ++j) {
