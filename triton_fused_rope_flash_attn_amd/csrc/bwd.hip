@@ -324,21 +324,16 @@ bwd_dq_kernel(const BwdParams p) {
     }
 
     for (int j = 0; j < rows / 32; ++j) {
-      // The logit accumulators (rows = keys kbase + 4h + i of this lane) start
-      // at 0 for keys < N and -inf beyond, so P = exp2(S*c - LSE2) is 0 there
-      // with no per-element select; the dP accumulators start at -delta of the
+      // Keys >= N (the rest of the block holding key N-1) need no mask: their
+      // K-hat and V rows are zero, so S = dP = 0 there and P, dS are finite
+      // (P is clamped to [0, 1], which the exact P never leaves, in the
+      // exponential's own clamp bit), and their dS^T entries meet zero K-hat
+      // rows in the dQ product.  The dP accumulators start at -delta of the
       // lane's query, so dP - delta needs no subtraction.
-      const int kbase = kvb + 32 * j + 8 * lg;
-      f32x4 kmask[2];
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kmask[h][i] = kbase + 4 * h + i < N ? 0.f : -INFINITY;
       f32x4 sacc[QT][2], pacc[QT][2];
 #pragma unroll
       for (int t = 0; t < QT; ++t) {
-        sacc[t][0] = kmask[0];
-        sacc[t][1] = kmask[1];
+        sacc[t][0] = sacc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
         pacc[t][0] = pacc[t][1] = f32x4{-dlt[t], -dlt[t], -dlt[t], -dlt[t]};
       }
 #pragma unroll
@@ -367,8 +362,9 @@ bwd_dq_kernel(const BwdParams p) {
         for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            ds[4 * h + i] = fast_exp2(FS ? __builtin_fmaf(sacc[t][h][i], fsc, -lse2[t])
-                                         : sacc[t][h][i] - lse2[t]) * pacc[t][h][i];
+            ds[4 * h + i] = __builtin_amdgcn_fmed3f(
+                                fast_exp2(FS ? __builtin_fmaf(sacc[t][h][i], fsc, -lse2[t])
+                                             : sacc[t][h][i] - lse2[t]), 0.f, 1.f) * pacc[t][h][i];
         if constexpr (FS)
           split_bf16x8(ds, dsf[t].v, dsfl[t].v);
         else
