@@ -488,8 +488,7 @@ __device__ __forceinline__ float group4_max(float v) { return xor32_pair_op_max(
 // Largest of a non-negative float over the wave, as its fp32 bit pattern
 // (those order like the values), in every lane: DPP within each 16-lane row
 // (both quad permutations, then the mirror images within the half row and
-// the row), then the two row swaps.  (No __shfl: those are device-library
-// calls that these kernels, built with IEEE mode off, would not inline.)
+// the row), then the two row swaps -- VALU only, no LDS round trip.
 __device__ __forceinline__ unsigned wave_max_bits(float x) {
   x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false)));
   x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false)));
