@@ -67,6 +67,19 @@ __device__ __forceinline__ int kperm(int r) {
   return (r & ~31) | ((r & 4) << 2) | ((r & 24) >> 1) | (r & 3);
 }
 
+// Physical LDS row of key r in the row-major V tile (16-bit compute): within
+// each 16-row half c of a 32-key block, r = 16c + 8a + 4h + i is stored at
+// 16c + 2 (i%2 + 2a + 4 (i/2)) + h.  The transposed V^T reads of one 32-lane
+// half (keys 8lg + 0..3 and 8lg + 8..11, lg = 0, 1; or the same + 4) then hit
+// eight rows of one parity, whose 8-word segments at a pitch of 4 mod 8 words
+// (D + 8 elements) fall on disjoint banks, and the staging writes of rows r
+// and r + 2 by one 16-lane group land 8 rows (32 words mod 64 at D = 64)
+// apart: both conflict-free in a 64-bank model, against 2-way in key order.
+__device__ __forceinline__ int vperm(int r) {
+  const int i = r & 3, h = (r >> 2) & 1, a = (r >> 3) & 1;
+  return (r & ~15) | (2 * ((i & 1) + 2 * a + 4 * (i >> 1)) + h);
+}
+
 // V^T tile: the 8-key group g of channel row d is stored at group
 // g ^ ((d >> 3) & 7).  With a row pitch of KC + 16 elements this makes both
 // the transposed stores (8 channel rows x 2 key pairs per 16 lanes) and the
@@ -132,9 +145,7 @@ fwd_kernel(const FwdParams p) {
   const bool vec_v = VEC || p.vec_v, vec_o = VEC || p.vec_o;
   const int shift = 1 - p.has_cls;    // table row of token s is s + shift
   const float c2 = p.scale_log2;
-  // cos/sin of pairs p0 .. p0+3 of table row `row`.  `swap` lanes fetch the
-  // two 16-byte halves in the opposite order (spreads banks when neighbouring
-  // lanes read the same columns of two rows).
+  // cos/sin of pairs p0 .. p0+3 of table row `row`.
   auto tab4 = [&](int row, int p0, float (&cs)[8]) __attribute__((always_inline)) {
     if constexpr (kTabLds) {
       const int c = p0 >> 1;   // chunks c, c + 1 hold pairs p0 .. p0+3
@@ -154,6 +165,12 @@ fwd_kernel(const FwdParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (SGPR)
   const int lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
+  // V tile rows of the lane's two transposed reads per 32-key block (see
+  // vperm; key order where the two row constants would not fit the generic
+  // D = 128 path's registers)
+  constexpr bool kVperm = sizeof(S) == 2 && (VEC || D <= 64);
+  auto vrow = [](int r) { return kVperm ? vperm(r) : r; };
+  const int vr0 = vrow(8 * lg + (lr >> 2)), vr1 = vrow(8 * lg + 4 + (lr >> 2));
 
   // Item of this workgroup at iteration `it` (-1 when done).  Within an
   // iteration, items are dealt XCD-major so neighbouring items (the q blocks
@@ -311,7 +328,7 @@ fwd_kernel(const FwdParams p) {
             C::put8(&sK[slot][kperm(2 * rp + x) * LDK + 8 * cc], xk);
           }
           if constexpr (TRV || VROW) {
-            S* dst = &sVt[slot][(2 * rp + x) * LDK + 8 * cc];
+            S* dst = &sVt[slot][vrow(2 * rp + x) * LDK + 8 * cc];
             if constexpr (std::is_same<IO, S>::value) {
               *reinterpret_cast<typename Raw8<IO>::vec*>(dst) = pv[it][x].v;   // raw row segment
             } else {
@@ -452,8 +469,8 @@ fwd_kernel(const FwdParams p) {
 #pragma unroll
     for (int d = 0; d < DT; ++d) {
       if constexpr (TRV)
-        vf[d] = C::tr(cV + tr_offset(32 * j + 8 * lg, 16 * d, LDK, lr),
-                      cV + tr_offset(32 * j + 8 * lg + 4, 16 * d, LDK, lr));
+        vf[d] = C::tr(cV + (32 * j + vr0) * LDK + 16 * d + 4 * (lr & 3),
+                      cV + (32 * j + vr1) * LDK + 16 * d + 4 * (lr & 3));
       else if constexpr (VROW)
         vf[d] = vrow_frag(cV, j, d);
       else
@@ -681,7 +698,7 @@ fwd_kernel(const FwdParams p) {
       // A = V^T rows 16d.., k-slot e <-> key 32j + 8lg + e (the P^T order)
       Frag a;
       if constexpr (TRV)
-        a = C::tr(cV + tr_offset(32 * j + 8 * lg, 16 * d, LDK, lr), cV + tr_offset(32 * j + 8 * lg + 4, 16 * d, LDK, lr));
+        a = C::tr(cV + (32 * j + vr0) * LDK + 16 * d + 4 * (lr & 3), cV + (32 * j + vr1) * LDK + 16 * d + 4 * (lr & 3));
       else if constexpr (VROW)
         a = vrow_frag(cV, j, d);
       else
