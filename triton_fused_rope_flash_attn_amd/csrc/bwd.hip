@@ -501,6 +501,10 @@ bwd_dkdv_kernel(const BwdParams p) {
   const int wave = tid >> 6, lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
   const int kv_first = kblk * KROWS + wave * KT * 16;
+  // 16-bit tiles: LDS row of staged query r (see vperm: conflict-free
+  // transposed reads), and the rows of the lane's two transposed reads
+  auto qrow = [](int r) { return TR ? vperm(r) : r; };
+  const int qt0 = qrow(8 * lg + (lr >> 2)), qt1 = qrow(8 * lg + 4 + (lr >> 2));
   // LSE (natural log) -> the S accumulators' seed -LSE2 (FS: times fq fk)
   const float l2seed = FS ? kLog2e * fq * fk : kLog2e;
   // ---- this wave's K-hat and V rows as B-operands ----
@@ -606,8 +610,8 @@ bwd_dkdv_kernel(const BwdParams p) {
         const float cs[8] = {pt[it][0][0], pt[it][0][1], pt[it][0][2], pt[it][0][3],
                              pt[it][1][0], pt[it][1][1], pt[it][1][2], pt[it][1][3]};
         rope_rotate8(xq, cs);
-        put_qhat(r * LDQ + 8 * cc, xq);
-        C::put8(&sG[r * LDQ + 8 * cc], xg);
+        put_qhat(qrow(r) * LDQ + 8 * cc, xq);
+        C::put8(&sG[qrow(r) * LDQ + 8 * cc], xg);
         if constexpr (!TR) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
@@ -654,8 +658,8 @@ bwd_dkdv_kernel(const BwdParams p) {
         const int r = c / CPR, cc = c - r * CPR;
         if (c < rows * CPR) {
           rope_rotate8(xq[it], cs[it]);
-          put_qhat(r * LDQ + 8 * cc, xq[it]);
-          C::put8(&sG[r * LDQ + 8 * cc], xg[it]);
+          put_qhat(qrow(r) * LDQ + 8 * cc, xq[it]);
+          C::put8(&sG[qrow(r) * LDQ + 8 * cc], xg[it]);
           if constexpr (!TR) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -687,7 +691,7 @@ bwd_dkdv_kernel(const BwdParams p) {
         for (int s = 0; s < KS; ++s) {
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
-            const int ql = 32 * j + 8 * (lr >> 2) + 4 * h + (lr & 3);
+            const int ql = 32 * j + qrow(8 * (lr >> 2) + 4 * h + (lr & 3));
             LFrag a;
             if constexpr (FS)
               a = LC::lds(&sQf[ql * LDQ + 32 * s + 8 * lg]);
@@ -727,8 +731,8 @@ bwd_dkdv_kernel(const BwdParams p) {
           // A = dO^T / Q-hat^T rows 16d.., k-slot e <-> query 32j + 8lg + e (the P / dS order)
           Frag ag, aq;
           if constexpr (TR) {
-            const int o0 = tr_offset(32 * j + 8 * lg, 16 * d, LDQ, lr);
-            const int o1 = tr_offset(32 * j + 8 * lg + 4, 16 * d, LDQ, lr);
+            const int o0 = (32 * j + qt0) * LDQ + 16 * d + 4 * (lr & 3);
+            const int o1 = (32 * j + qt1) * LDQ + 16 * d + 4 * (lr & 3);
             ag = C::tr(&sG[o0], &sG[o1]);
             aq = C::tr(&sQ[o0], &sQ[o1]);
           } else {

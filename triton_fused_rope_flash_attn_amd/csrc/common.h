@@ -228,6 +228,20 @@ __device__ __forceinline__ s16x4 lds_tr4(const void* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
 }
 
+// Physical LDS row of row r of a row-major 16-bit tile that is read transposed
+// (the forward's V, the dK/dV kernel's Q-hat and dO): within each 16-row
+// half c of a 32-row block, r = 16c + 8a + 4h + i is stored at
+// 16c + 2 (i%2 + 2a + 4 (i/2)) + h.  The transposed reads of one 32-lane half
+// (rows 8lg + 0..3 and 8lg + 8..11, lg = 0, 1; or the same + 4) then hit
+// eight rows of one parity, whose 8-word segments at a pitch of 4 mod 8 words
+// (D + 8 elements) fall on disjoint banks, and the staging writes of rows r
+// and r + 2 by one 16-lane group land 8 rows (32 words mod 64 at D = 64)
+// apart: both conflict-free in a 64-bank model, against 2-way in key order.
+__device__ __forceinline__ int vperm(int r) {
+  const int i = r & 3, h = (r >> 2) & 1, a = (r >> 3) & 1;
+  return (r & ~15) | (2 * ((i & 1) + 2 * a + 4 * (i >> 1)) + h);
+}
+
 // Element offset, inside a row-major tile of pitch `ld`, that lane (lr, lg)
 // addresses so that the read yields rows r0 + e (e = 0..3) of column c0 + lr.
 __device__ __forceinline__ int tr_offset(int r0, int c0, int ld, int lr) {

@@ -67,19 +67,6 @@ __device__ __forceinline__ int kperm(int r) {
   return (r & ~31) | ((r & 4) << 2) | ((r & 24) >> 1) | (r & 3);
 }
 
-// Physical LDS row of key r in the row-major V tile (16-bit compute): within
-// each 16-row half c of a 32-key block, r = 16c + 8a + 4h + i is stored at
-// 16c + 2 (i%2 + 2a + 4 (i/2)) + h.  The transposed V^T reads of one 32-lane
-// half (keys 8lg + 0..3 and 8lg + 8..11, lg = 0, 1; or the same + 4) then hit
-// eight rows of one parity, whose 8-word segments at a pitch of 4 mod 8 words
-// (D + 8 elements) fall on disjoint banks, and the staging writes of rows r
-// and r + 2 by one 16-lane group land 8 rows (32 words mod 64 at D = 64)
-// apart: both conflict-free in a 64-bank model, against 2-way in key order.
-__device__ __forceinline__ int vperm(int r) {
-  const int i = r & 3, h = (r >> 2) & 1, a = (r >> 3) & 1;
-  return (r & ~15) | (2 * ((i & 1) + 2 * a + 4 * (i >> 1)) + h);
-}
-
 // V^T tile: the 8-key group g of channel row d is stored at group
 // g ^ ((d >> 3) & 7).  With a row pitch of KC + 16 elements this makes both
 // the transposed stores (8 channel rows x 2 key pairs per 16 lanes) and the
