@@ -228,15 +228,15 @@ __device__ __forceinline__ s16x4 lds_tr4(const void* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
 }
 
-// Physical LDS row of row r of a row-major 16-bit tile that is read transposed
-// (the forward's V, the dK/dV kernel's Q-hat and dO): within each 16-row
+// Physical LDS row of row r of the forward's V tile and of the dK/dV kernel's
+// staged Q-hat / dO tiles (16-bit, pitch D + 8 elements): within each 16-row
 // half c of a 32-row block, r = 16c + 8a + 4h + i is stored at
-// 16c + 2 (i%2 + 2a + 4 (i/2)) + h.  The transposed reads of one 32-lane half
-// (rows 8lg + 0..3 and 8lg + 8..11, lg = 0, 1; or the same + 4) then hit
-// eight rows of one parity, whose 8-word segments at a pitch of 4 mod 8 words
-// (D + 8 elements) fall on disjoint banks, and the staging writes of rows r
-// and r + 2 by one 16-lane group land 8 rows (32 words mod 64 at D = 64)
-// apart: both conflict-free in a 64-bank model, against 2-way in key order.
+// 16c + 2 (i%2 + 2a + 4 (i/2)) + h.  Timed on gfx950, this runs the 16-byte
+// operand-row reads of the dK/dV kernel (rows 8 (l/4) + 4h + l%4 of 16
+// lanes) at the conflict-free rate instead of 1.45x, and its transposed reads
+// at 1.35x instead of 1.0x; in that kernel the trade measured -3.3% of the
+// backward.  (For the forward's V, which has only the transposed reads, it
+// measured neutral.)
 __device__ __forceinline__ int vperm(int r) {
   const int i = r & 3, h = (r >> 2) & 1, a = (r >> 3) & 1;
   return (r & ~15) | (2 * ((i & 1) + 2 * a + 4 * (i >> 1)) + h);
