@@ -323,19 +323,16 @@ bwd_dq_kernel(const BwdParams p) {
     if (!wave_active) continue;
     }
 
-    for (int j = 0; j < rows / 32; ++j) {
-      // Keys >= N (the rest of the block holding key N-1) need no mask: their
-      // K-hat and V rows are zero, so S = dP = 0 there and P, dS are finite
-      // (P is clamped to [0, 1], which the exact P never leaves, in the
-      // exponential's own clamp bit), and their dS^T entries meet zero K-hat
-      // rows in the dQ product.  The dP accumulators start at -delta of the
-      // lane's query, so dP - delta needs no subtraction.
-      f32x4 sacc[QT][2], pacc[QT][2];
+    // Keys >= N (the rest of the block holding key N-1) need no mask: their
+    // K-hat and V rows are zero, so S = dP = 0 there and P, dS are finite
+    // (P is clamped to [0, 1], which the exact P never leaves, in the
+    // exponential's own clamp bit), and their dS^T entries meet zero K-hat
+    // rows in the dQ product.  The dP accumulators start at -delta of the
+    // lane's query, so dP - delta needs no subtraction.
+    // S (logits) and dP of key block j, as two separate product sets:
+    auto s_of = [&](int j, f32x4 (&sacc)[QT][2]) __attribute__((always_inline)) {
 #pragma unroll
-      for (int t = 0; t < QT; ++t) {
-        sacc[t][0] = sacc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-        pacc[t][0] = pacc[t][1] = f32x4{-dlt[t], -dlt[t], -dlt[t], -dlt[t]};
-      }
+      for (int t = 0; t < QT; ++t) sacc[t][0] = sacc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
 #pragma unroll
@@ -346,14 +343,27 @@ bwd_dq_kernel(const BwdParams p) {
             a = LC::lds(&sKf[kl * LDK + 32 * s + 8 * lg]);
           else
             a = C::lds(&sK[kl * LDK + 32 * s + 8 * lg]);
-          const Frag b = C::lds(&sV[kl * LDK + 32 * s + 8 * lg]);
 #pragma unroll
-          for (int t = 0; t < QT; ++t) {
-            sacc[t][h] = LC::mma(a, qf[t][s], sacc[t][h]);
-            pacc[t][h] = C::mma(b, gf[t][s], pacc[t][h]);
-          }
+          for (int t = 0; t < QT; ++t) sacc[t][h] = LC::mma(a, qf[t][s], sacc[t][h]);
         }
       }
+    };
+    auto p_of = [&](int j, f32x4 (&pacc)[QT][2]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int t = 0; t < QT; ++t) pacc[t][0] = pacc[t][1] = f32x4{-dlt[t], -dlt[t], -dlt[t], -dlt[t]};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int kl = 32 * j + 8 * (lr >> 2) + 4 * h + (lr & 3);
+          const Frag b = C::lds(&sV[kl * LDK + 32 * s + 8 * lg]);
+#pragma unroll
+          for (int t = 0; t < QT; ++t) pacc[t][h] = C::mma(b, gf[t][s], pacc[t][h]);
+        }
+      }
+    };
+    // dS of key block j from its S / dP, then dQ-hat^T += K-hat^T dS^T:
+    auto pq = [&](int j, const f32x4 (&sacc)[QT][2], const f32x4 (&pacc)[QT][2]) __attribute__((always_inline)) {
       Frag dsf[QT], dsfl[FS ? QT : 1];
 #pragma unroll
       for (int t = 0; t < QT; ++t) {
@@ -385,6 +395,20 @@ bwd_dq_kernel(const BwdParams p) {
           dqacc[t][d] = C::mma(a, dsf[t], dqacc[t][d]);
         }
       }
+    };
+    // Two key blocks per trip: the logits of block j+1 go to the MFMA pipe
+    // before block j's dS is computed on the VALU, its dP after (two blocks'
+    // S and dP accumulators together do not fit the registers).  A ragged
+    // last block recomputes block j instead and skips its update.
+    const int nbj = rows / 32;
+    for (int j = 0; j < nbj; j += 2) {
+      f32x4 sA[QT][2], pA[QT][2], sB[QT][2], pB[QT][2];
+      s_of(j, sA);
+      p_of(j, pA);
+      s_of(min(j + 1, nbj - 1), sB);
+      pq(j, sA, pA);
+      p_of(min(j + 1, nbj - 1), pB);
+      if (j + 1 < nbj) pq(j + 1, sB, pB);
     }
   }
 
