@@ -336,9 +336,12 @@ int farope_attn_fwd(const farope_attn_desc* desc, const void* q, const int64_t q
   const int tail = tail_of(p.B * p.H, p.N, rows);
   p.n_blk = main_blocks(p.B * p.H, p.N, rows);
   p.n_items = p.B * p.H * p.n_blk;
+  const bool vec = p.vec_q && p.vec_k && p.vec_v && p.vec_o;
+  p.x_rows = tail == 1 && fwd_folds_tail(desc->io_dtype, desc->compute_dtype, desc->head_dim, vec);
   const hipStream_t st = static_cast<hipStream_t>(stream);
   FAROPE_TRY(launch_rc(launch_fwd(p, desc->io_dtype, desc->compute_dtype, desc->head_dim, st)));
-  if (tail) FAROPE_TRY(launch_rc(launch_fwd_tail(p, desc->io_dtype, desc->head_dim, p.N - tail, st)));
+  if (tail && !p.x_rows)
+    FAROPE_TRY(launch_rc(launch_fwd_tail(p, desc->io_dtype, desc->head_dim, p.N - tail, st)));
   return FAROPE_OK;
 }
 

@@ -120,6 +120,19 @@ fwd_kernel(const FwdParams p) {
   // FS: per-wave max |Q-hat|, max |K-hat| bit patterns of an item pass
   __shared__ u32x2 sRange[FS ? NW : 1];
   __shared__ __attribute__((aligned(16))) S sVt[2][(TRV || VROW) ? KC * LDK : D * LDV];
+  // XR: the plane's last row, when it is the only one past the full query
+  // blocks (p.x_rows == 1, N = 1 + a multiple of the block rows), rides along
+  // one designated item of the plane instead of a tail kernel that would read
+  // the whole plane's K and V again.  Its logits and O run on the VALU against
+  // the same staged K-hat / V chunks: wave w takes keys KC/NW * w .. of each
+  // chunk, keeps its own online-softmax state in LDS, and the NW partial
+  // states merge at the item's end.  Its Q-hat row is staged like the others
+  // (fp16, scaled by c2 * fq, counted in the operand range).
+  constexpr bool XR = FS && VEC && sizeof(IO) == 2 && KC == 8 * NW;
+  constexpr int XO = XR ? D / 64 : 1;  // output channels per lane (XR)
+  __shared__ __attribute__((aligned(16))) f16 sXq[XR ? 2 : 1][XR ? D : 8];   // by pass parity
+  __shared__ __attribute__((aligned(16))) float sXo[XR ? NW : 1][XR ? D : 4];
+  __shared__ float sXml[XR ? NW : 1][2];
   // LDS copy of the packed table: D/2 (cos, sin) pairs = D floats per row,
   // 16-byte chunk c of row r stored at chunk c ^ (r & (D/4 - 1)) (bank-spread
   // without padding).
@@ -380,6 +393,8 @@ fwd_kernel(const FwdParams p) {
     }
   };
   LFrag qf[QT][KS];
+  bool xi = false;   // XR: this item pass also computes the plane's last row
+  int npass = 0;     // item passes so far (a rescaled pass counts again)
   auto commit_q = [&](int plane, int qb) __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < QT; ++t)
@@ -419,6 +434,67 @@ fwd_kernel(const FwdParams p) {
           qf[t][s] = C::make(x);
         }
       }
+    if constexpr (XR) {
+      if (xi && wave == 0 && lane < D / 8) {
+        const int c0 = 8 * opaque(lane);
+        float x[8], cs[8];
+        unpack8(load_raw8(plane_base(p.q, p.sq, plane) + (N - 1) * p.sq[2] + c0, 1, true), x);
+        rope_load4(p.rope, N - 1 + shift, D2, c0 / 2, cs);
+        rope_rotate8(x, cs);
+        const float qs = c2 * fq;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] *= qs;
+        amax_q = amax8(amax_q, x);
+        *reinterpret_cast<f16x8*>(&sXq[npass & 1][c0]) = to_f16x8(x);
+      }
+    }
+  };
+  // XR: the last row against keys kvb + 8 * wave + (0..7) of a staged chunk.
+  // Lane (key kk = lane / 8, slice ds = lane % 8) forms the fp16 dot product
+  // over channels D/8 * ds .. of its key; then every lane updates channels
+  // XO * lane .. of the wave's partial O with the 8 probabilities.
+  auto xrow_chunk = [&](const S* __restrict__ cK, const S* __restrict__ cV, int kvb, bool first)
+      __attribute__((always_inline)) {
+    // (lane addresses from an opaque copy: recomputed here, not kept live
+    // through the chunk loop)
+    const int ln = opaque(lane);
+    const int kk = ln >> 3, ds = ln & 7;
+    const int r = 8 * wave + kk;
+    const f16* kp = reinterpret_cast<const f16*>(cK) + kperm(r) * LDK + (D / 8) * ds;
+    const f16* qp = &sXq[npass & 1][(D / 8) * ds];
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < D / 64; ++i)
+      s = dot8<f16>(*reinterpret_cast<const Raw8<f16>*>(qp + 8 * i), *reinterpret_cast<const Raw8<f16>*>(kp + 8 * i), s);
+    s = dpp_sum8(s);
+    s = kvb + r < N ? s * fsc : -INFINITY;
+    // the wave's 8 keys sit 8 lanes apart: row rotation by 8, then the row swaps
+    float cm = fmaxf(s, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x128, 0xF, 0xF, false)));
+    cm = group4_max(cm);
+    const float mo = first ? -INFINITY : sXml[wave][0];
+    const float lo = first ? 0.f : sXml[wave][1];
+    const float mn = fmaxf(mo, cm);
+    const float mb = mn == -INFINITY ? 0.f : mn;   // no valid key yet: all terms stay 0
+    const float al = fast_exp2(mo - mb);
+    const float pk = fast_exp2(s - mb);
+    float ps = pk + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(pk), 0x128, 0xF, 0xF, false));
+    ps = group4_sum(ps);
+    float o[XO];
+#pragma unroll
+    for (int i = 0; i < XO; ++i) o[i] = first ? 0.f : sXo[wave][XO * ln + i] * al;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pk), 8 * j));
+      const S* vp = cV + vrow(8 * wave + j) * LDK + XO * ln;
+#pragma unroll
+      for (int i = 0; i < XO; ++i) o[i] = __builtin_fmaf(pj, (float)vp[i], o[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < XO; ++i) sXo[wave][XO * ln + i] = o[i];
+    if (ln == 0) {
+      sXml[wave][0] = mn;
+      sXml[wave][1] = __builtin_fmaf(lo, al, ps);
+    }
   };
 
   float m_run[QT], l_run[QT], m_thr[QT];
@@ -825,6 +901,11 @@ fwd_kernel(const FwdParams p) {
   while (item >= 0) {
     const int plane = item / p.n_blk, qb = item - plane * p.n_blk;
     const int nxt = item_of(it + 1);
+    if constexpr (XR) {
+      // the designated item of a plane cycles through the q blocks with the
+      // plane's launch iteration, so the extra rows spread over workgroups
+      xi = p.x_rows != 0 && qb == (plane / max(1, p.n_wg / p.n_blk)) % p.n_blk;
+    }
     commit_q(plane, qb);
     int nt = 0;   // active subtiles of this wave: a prefix t < nt (wave-uniform)
 #pragma unroll
@@ -899,6 +980,9 @@ fwd_kernel(const FwdParams p) {
         mem();
         lds_barrier();
         if (nt > 0) chunk_serial(sK[slot], sVt[slot], chunk_start(c));
+        if constexpr (XR) {
+          if (xi) xrow_chunk(sK[slot], sVt[slot], chunk_start(c), c == 0);
+        }
       }
       ++g;
     };
@@ -909,6 +993,7 @@ fwd_kernel(const FwdParams p) {
       // a rescaled second pass (its first chunk is already on the way; no
       // Q prefetch or deferred store exists with these operands); no store
       amax_q = amax_k = 0.f;
+      if constexpr (XR) ++npass;
       if (redo) {
         redo = false;
         rescaled = true;
@@ -919,6 +1004,42 @@ fwd_kernel(const FwdParams p) {
       }
       rescaled = false;
       fq = fk = fsc = 1.f;
+    }
+    if constexpr (XR) {
+      if (xi) {
+        // merge the waves' partial states of the last row: M = max m_w,
+        // L = sum l_w 2^(m_w - M), O = sum o_w 2^(m_w - M) / L
+        lds_barrier();
+        if (wave == 0) {
+          const int ln = opaque(lane);
+          float M = -INFINITY;
+#pragma unroll
+          for (int w = 0; w < NW; ++w) M = fmaxf(M, sXml[w][0]);
+          float L = 0.f, o[XO] = {};
+#pragma unroll
+          for (int w = 0; w < NW; ++w) {
+            const float a = fast_exp2(sXml[w][0] - M);
+            L = __builtin_fmaf(sXml[w][1], a, L);
+#pragma unroll
+            for (int i = 0; i < XO; ++i) o[i] = __builtin_fmaf(sXo[w][XO * ln + i], a, o[i]);
+          }
+          const float inv = 1.f / L;
+          IO* orow_p = const_cast<IO*>(plane_base(p.o, p.so, plane)) + (N - 1) * p.so[2] + XO * ln;
+          typedef IO iox __attribute__((ext_vector_type(XO)));
+          iox h, rr;
+#pragma unroll
+          for (int i = 0; i < XO; ++i) {
+            o[i] *= inv;
+            h[i] = (IO)o[i];
+            rr[i] = (IO)(o[i] - (float)h[i]);
+          }
+          *reinterpret_cast<iox*>(orow_p) = h;
+          if constexpr (RES) {
+            if (p.o_res) *reinterpret_cast<iox*>(static_cast<IO*>(p.o_res) + ((int64_t)plane * N + N - 1) * D + XO * ln) = rr;
+          }
+          if (ln == 0) p.lse[(int64_t)plane * N + N - 1] = (M + fast_log2(L)) * kLn2;
+        }
+      }
     }
 
     // ---- epilogue: lane holds O[row][16d + 4lg + (0..3)] ----
@@ -1097,6 +1218,11 @@ static hipError_t fwd_ct(const FwdParams& p, int ct, int D, hipStream_t st) {
     case DT_F16: return fwd_shape<IO, DT_F16>(p, D, st);
     default: return fwd_shape<IO, DT_F32>(p, D, st);
   }
+}
+
+bool fwd_folds_tail(int io, int ct, int D, bool vec) {
+  // the XR instantiations: 16-bit I/O, fp16 logits, KC = 8 NW (D = 128, 256)
+  return io != DT_F32 && f16_logits(ct, D) && vec && (D == 128 || D == 256);
 }
 
 hipError_t launch_fwd(const FwdParams& p, int io, int ct, int D, hipStream_t st) {

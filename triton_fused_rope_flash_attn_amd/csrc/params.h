@@ -24,6 +24,7 @@ struct FwdParams {
   int n_blk;           // q blocks per plane
   int n_items;         // planes * n_blk work items
   int n_wg;            // workgroups of the launch (set by the launcher)
+  int x_rows;          // 1: the block kernel also computes row N - 1 (fwd_folds_tail)
 };
 
 struct BwdParams {
@@ -76,6 +77,10 @@ hipError_t launch_fwd_tail(const FwdParams& p, int io, int D, int row0, hipStrea
 hipError_t launch_bwd_tail_rows(const BwdParams& p, int io, int D, int row0, bool write_delta,
                                 hipStream_t st);
 hipError_t launch_bwd_tail_keys(const BwdParams& p, int io, int D, int key0, hipStream_t st);
+// Whether the forward block kernel computes a single tail row itself
+// (FwdParams::x_rows = 1) instead of launch_fwd_tail: fp16 logit operands with
+// vector access (vec: every tensor of the call allows it).
+bool fwd_folds_tail(int io, int ct, int D, bool vec);
 
 // fp16 logit operands and split dS: bf16 compute at head_dim >= 128.
 // Rounding the rotated Q / K rows to bf16 before the logits product is the
