@@ -166,8 +166,10 @@ int dq_pass(BwdParams p, const farope_attn_desc* d, bool write_delta, hipStream_
   const int D = d->head_dim, rows = bwd_dq_block_rows(D, d->compute_dtype);
   const int tail = tail_of(p.B * p.H, p.N, rows);
   p.n_blk = main_blocks(p.B * p.H, p.N, rows);
+  p.x_rows = tail == 1 && bwd_folds_tail(d->io_dtype, d->compute_dtype, D, p.vec_k && p.vec_v);
   FAROPE_TRY(launch_rc(launch_bwd_dq(p, d->io_dtype, d->compute_dtype, D, write_delta, st)));
-  if (tail) FAROPE_TRY(launch_rc(launch_bwd_tail_rows(p, d->io_dtype, D, p.N - tail, write_delta, st)));
+  if (tail && !p.x_rows)
+    FAROPE_TRY(launch_rc(launch_bwd_tail_rows(p, d->io_dtype, D, p.N - tail, write_delta, st)));
   return FAROPE_OK;
 }
 

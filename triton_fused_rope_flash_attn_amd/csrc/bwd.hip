@@ -104,11 +104,26 @@ bwd_dq_kernel(const BwdParams p) {
   __shared__ __attribute__((aligned(16))) S sKt[TR ? 8 : D * LDT];
   __shared__ __attribute__((aligned(16))) S sV[KVS * LDK];
   __shared__ u32x2 sRange[FS ? NW : 1];   // FS: per-wave max |Q-hat|, |K-hat| bits
+  // XR: the plane's last row, when it is the only one past the full query
+  // blocks (p.x_rows == 1), rides along one tile of the plane instead of a
+  // tail kernel that would read the plane's K and V again.  Its logits, dP
+  // and dQ run on the VALU against the staged key blocks: wave w takes keys
+  // KVS/NW * w .. of each block and keeps a partial dQ row in LDS; the
+  // partial rows are summed at the tile's end.  Its Q-hat (fp16, scaled
+  // like the other rows and counted in the operand range), dO and delta are
+  // staged once per pass.
+  constexpr bool XR = FS && VEC && sizeof(IO) == 2 && KVS == 8 * NW;
+  constexpr int XO = XR ? D / 64 : 1;   // dQ channels per lane (XR)
+  __shared__ __attribute__((aligned(16))) f16 sXq[XR ? D : 8];
+  __shared__ __attribute__((aligned(16))) S sXg[XR ? D : 8];
+  __shared__ __attribute__((aligned(16))) float sXo[XR ? NW : 1][XR ? D : 4];
+  __shared__ float sXd[2];   // delta, LSE2 of the last row
 
   const int N = p.N;
   const int tile = xcd_remap(block_id(), p.n_wg);
   const int plane = tile / p.n_blk;
   const int qblk = tile - plane * p.n_blk;
+  const bool xi = XR && p.x_rows != 0 && qblk == plane % p.n_blk;
   const int bb = plane / p.H, hh = plane - bb * p.H;
   const IO* __restrict__ Q = static_cast<const IO*>(p.q) + bb * p.sq[0] + hh * p.sq[1];
   const IO* __restrict__ K = static_cast<const IO*>(p.k) + bb * p.sk[0] + hh * p.sk[1];
@@ -187,6 +202,46 @@ bwd_dq_kernel(const BwdParams p) {
       dlt[t] = row < N ? p.delta[prow + row] : 0.f;
     }
     lse2[t] = row < N ? p.lse[prow + row] * kLog2e : 0.f;
+  }
+  if constexpr (XR) {
+    if (xi && wave == 0 && lane < D / 8) {
+      const int row = N - 1, c0 = 8 * opaque(lane);
+      float x[8], g[8], cs[8];
+      load8(Q + row * p.sq[2] + c0 * p.sq[3], p.sq[3], p.vec_q, x);
+      rope_load4(tab, row + shift, D2, c0 / 2, cs);
+      rope_rotate8(x, cs);
+      const float qs = p.scale_log2 * fq;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] *= qs;
+      amax_q = amax8(amax_q, x);
+      *reinterpret_cast<f16x8*>(&sXq[c0]) = to_f16x8(x);
+      load8(G + row * p.sdo[2] + c0 * p.sdo[3], p.sdo[3], p.vec_do, g);
+      C::put8(&sXg[c0], g);
+      float dsum;
+      if (WRITE_DELTA) {
+        float o[8];
+        load8(O + row * p.so[2] + c0 * p.so[3], p.so[3], p.vec_o, o);
+        dsum = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dsum += g[e] * o[e];
+        if (p.o_res) {
+          load8(static_cast<const IO*>(p.o_res) + (prow + row) * D + c0, 1, true, o);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dsum += g[e] * o[e];
+        }
+        // over the D/8 active lanes: 8-lane groups, then rows of 16, then row pairs
+        dsum = dpp_sum8(dsum);
+        dsum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(dsum), 0x128, 0xF, 0xF, false));
+        if constexpr (D / 8 >= 32) dsum = xor16_pair_op_sum(dsum);
+        if (lane == 0) p.delta[prow + row] = dsum;
+      } else {
+        dsum = p.delta[prow + row];
+      }
+      if (lane == 0) {
+        sXd[0] = dsum;
+        sXd[1] = p.lse[prow + row] * kLog2e;
+      }
+    }
   }
   if constexpr (FS) amax_q = opaque(amax_q);
   const bool wave_active = qblk * QROWS + wave * QT * 16 < N;
@@ -410,6 +465,38 @@ bwd_dq_kernel(const BwdParams p) {
       p_of(min(j + 1, nbj - 1), pB);
       if (j + 1 < nbj) pq(j + 1, sB, pB);
     }
+    if constexpr (XR) {
+      if (xi) {
+        // the last row against keys kvb + 8 * wave + (0..7): lane (key
+        // lane / 8, channel slice lane % 8) forms the fp16 logit and the dP
+        // dot products; every lane then adds the 8 dS-weighted K-hat rows
+        // to channels XO * lane .. of the wave's partial dQ.  Keys >= N have
+        // zero K-hat rows (no contribution), as in the block products.
+        const int kk = lane >> 3, ds = lane & 7, r = 8 * wave + kk;
+        float s = 0.f, dp = 0.f;
+#pragma unroll
+        for (int i = 0; i < D / 64; ++i) {
+          const int c = (D / 8) * ds + 8 * i;
+          s = dot8<f16>(*reinterpret_cast<const Raw8<f16>*>(&sXq[c]), *reinterpret_cast<const Raw8<f16>*>(&sKf[r * LDK + c]), s);
+          dp = dot8<S>(*reinterpret_cast<const Raw8<S>*>(&sXg[c]), *reinterpret_cast<const Raw8<S>*>(&sV[r * LDK + c]), dp);
+        }
+        s = dpp_sum8(s);
+        dp = dpp_sum8(dp);
+        const float dsx = __builtin_amdgcn_fmed3f(fast_exp2(__builtin_fmaf(s, fsc, -sXd[1])), 0.f, 1.f) * (dp - sXd[0]);
+        float o[XO];
+#pragma unroll
+        for (int i = 0; i < XO; ++i) o[i] = kvb == 0 ? 0.f : sXo[wave][XO * lane + i];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float dj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dsx), 8 * j));
+          const S* kb = &sK[(8 * wave + j) * LDK + XO * lane];
+#pragma unroll
+          for (int i = 0; i < XO; ++i) o[i] = __builtin_fmaf(dj, (float)kb[i], o[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < XO; ++i) sXo[wave][XO * lane + i] = o[i];
+      }
+    }
   }
 
   if constexpr (FS) {
@@ -438,10 +525,25 @@ bwd_dq_kernel(const BwdParams p) {
       continue;
     }
   }
+  if constexpr (XR) {
+    // (the range barrier above ordered every wave's partial dQ row)
+    if (xi && wave == 0 && lane < D / 4) {
+      const int ln = opaque(lane);   // (addresses formed here, not kept through the pass)
+      float g4[4] = {};
+#pragma unroll
+      for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) g4[r] += sXo[w][4 * ln + r];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) g4[r] *= dq_scale;
+      rope_unrotate4(g4, tab, N - 1 + shift, D2, 2 * ln);
+      store4(dQ + (N - 1) * p.sdq[2] + 4 * ln * p.sdq[3], p.sdq[3], p.vec_dq, g4);
+    }
+  }
 
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
-    const int row = qrow[t];
+    const int row = FS ? opaque(qrow[t]) : qrow[t];   // (FS: table address formed here)
     if (row < N) {
 #pragma unroll
       for (int d = 0; d < DT; ++d) {
@@ -956,6 +1058,12 @@ hipError_t launch_bwd_pre(const BwdParams& p, int io, int D, hipStream_t st) {
     case DT_F16: return pre_io<f16, 256>(p, st);
     default: return pre_io<float, 256>(p, st);
   }
+}
+
+bool bwd_folds_tail(int io, int ct, int D, bool vec) {
+  // the XR instantiations of the dQ kernel: 16-bit I/O, fp16 logits, 8 keys
+  // per wave and block (D = 128, 256)
+  return io != DT_F32 && f16_logits(ct, D) && vec && (D == 128 || D == 256);
 }
 
 template <typename IO, int CT, int D>

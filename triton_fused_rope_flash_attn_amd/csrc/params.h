@@ -47,6 +47,7 @@ struct BwdParams {
   int vec_q, vec_k, vec_v, vec_o, vec_do, vec_dq, vec_dk, vec_dv;
   int n_blk;           // q blocks (dq kernel) or kv blocks (dk/dv kernel) per plane
   int n_wg;            // workgroups of the launch (set by the launcher)
+  int x_rows;          // 1: the dQ block kernel also computes row N - 1 (bwd_folds_tail)
 };
 
 // Launch shapes picked by the tile table (api.hip).
@@ -81,6 +82,11 @@ hipError_t launch_bwd_tail_keys(const BwdParams& p, int io, int D, int key0, hip
 // (FwdParams::x_rows = 1) instead of launch_fwd_tail: fp16 logit operands with
 // vector access (vec: every tensor of the call allows it).
 bool fwd_folds_tail(int io, int ct, int D, bool vec);
+// The same for the dQ kernel's tail row (vec: K and V allow vector access),
+// instead of launch_bwd_tail_rows.  (The dK/dV kernel keeps its tail kernel:
+// the tail key's VALU work lengthens every query stage of its tile by more
+// than the tail kernel costs.)
+bool bwd_folds_tail(int io, int ct, int D, bool vec);
 
 // fp16 logit operands and split dS: bf16 compute at head_dim >= 128.
 // Rounding the rotated Q / K rows to bf16 before the logits product is the
