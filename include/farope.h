@@ -188,8 +188,10 @@ int farope_attn_bwd_noalloc(const farope_attn_desc* desc,
  * bwd: 0 fused, 1 split), out[1] = query (fwd) or key (bwd) rows per work
  * item, out[2] = work items per (b, h) plane, out[3] = threads per
  * workgroup.  When 1 to 8 rows are left past out[1] * out[2] (N = 1025 with
- * 128- or 256-row items), they are computed by the tail-row kernels rather
- * than by one more, nearly empty, work item.
+ * 128- or 256-row items), they are computed by the tail-row kernels (or, for
+ * a single row with fp16 logit operands, by one designated item of each plane
+ * in the forward and dQ block kernels) rather than by one more, nearly
+ * empty, work item.
  */
 int farope_tile_config(const farope_attn_desc* desc, int32_t which, int32_t out[4]);
 

@@ -195,8 +195,10 @@ def test_ragged_and_variant_shapes(side, has_cls, D):
 )
 def test_tail_rows(side, has_cls, D, B, H, io):
     """Rows past the last full block (N % block_rows <= 8, e.g. N = 16^2 + 1, 63^2 + 1,
-    62^2): computed by the tail kernels, not by a nearly empty block.  One tail row at
-    every head dim and I/O type; two (N = 3970, dK/dV) and four (N = 3844, no CLS) rows."""
+    62^2): computed by the tail kernels, or -- one row with fp16 logit operands (bf16,
+    D 128 / 256) -- by one designated item per plane of the forward and dQ block kernels,
+    not by a nearly empty block.  One tail row at every head dim and I/O type; two
+    (N = 3970, dK/dV) and four (N = 3844, no CLS) rows."""
     dt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[io]
     N = side * side + int(has_cls)
     code = _lib.DTYPE_CODE[dt]
