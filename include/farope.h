@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define FAROPE_ABI_VERSION 2
+#define FAROPE_ABI_VERSION 3
 
 typedef enum farope_dtype {
   FAROPE_F32 = 0,
@@ -96,6 +96,18 @@ int farope_rope_pack(const float* cosp, int64_t cos_stride0, int64_t cos_stride1
 size_t farope_attn_residual_elems(const farope_attn_desc* desc);
 
 /*
+ * fp32 elements of farope_attn_bwd's delta_ws: batch * heads * seq_len delta
+ * rows (the reference's D tensor, allocated with M's shape in
+ * TritonAttention.backward, FA:1075), plus, when each plane's last key
+ * is the only one past the dK/dV kernel's full key blocks at fp16-logit
+ * shapes (bf16 compute, head_dim 128 or 256, N = 1 + a multiple of 256), one
+ * partial dK / dV row pair per dQ tile: those tiles add that key's products
+ * over their own query rows instead of a kernel that re-reads the plane.
+ * 0 on an invalid descriptor.
+ */
+size_t farope_attn_bwd_workspace_elems(const farope_attn_desc* desc);
+
+/*
  * Forward: o = softmax(scale * (R q)(R k)^T) v, lse = logsumexp of the
  * scaled logits per row (natural log).  Replaces the _attn_fwd launch
  * (FA:1036-1057; kernel FA:91-315).  o_res: NULL, or a buffer of
@@ -143,7 +155,8 @@ int farope_attn_bwd_dq(const farope_attn_desc* desc,
  * Whole backward pass (what TritonAttention.backward does, FA:1067-1138):
  * picks the fused one-launch kernel when the plane fits on chip (D = 64,
  * N <= 256), else dq (which also writes delta) followed by dk/dv.
- * delta_ws: caller-owned fp32 workspace of batch*heads*seq_len elements.
+ * delta_ws: caller-owned fp32 workspace of
+ * farope_attn_bwd_workspace_elems(desc) elements.
  * o_res: NULL, or the residual buffer the forward filled.
  */
 int farope_attn_bwd(const farope_attn_desc* desc,

@@ -80,6 +80,28 @@ def test_tile_table(lib, N, D, has_cls, fwd_items, bwd_var):
     assert f[3] % 64 == 0 and b[3] % 64 == 0
 
 
+@pytest.mark.parametrize(
+    "B,H,N,D,io,ct,extra",
+    [
+        (32, 12, 1025, 128, _lib.BF16, _lib.BF16, 4 * 2 * 128),   # HiRes: 4 dQ tiles per plane
+        (2, 3, 257, 256, _lib.BF16, _lib.BF16, 4 * 2 * 256),      # 64-row dQ tiles
+        (2, 3, 257, 128, _lib.F16, _lib.BF16, 1 * 2 * 128),       # fp16 I/O, bf16 compute
+        (256, 12, 197, 64, _lib.BF16, _lib.BF16, 0),              # one-pass backward
+        (2, 3, 257, 64, _lib.BF16, _lib.BF16, 0),                 # no fp16 logits at D = 64
+        (2, 3, 257, 128, _lib.F16, _lib.F16, 0),                  # fp16 compute
+        (2, 3, 1100, 128, _lib.BF16, _lib.BF16, 0),               # 76 rows past the blocks
+        (2, 3, 3970, 128, _lib.BF16, _lib.BF16, 0),               # dQ blocks leave 130 rows
+    ],
+)
+def test_bwd_workspace_elems(lib, B, H, N, D, io, ct, extra):
+    """delta rows, plus one partial dK / dV row pair per dQ tile when the plane's
+    lone last key is summed by those tiles (fp16 logits, N = 1 + k * 256)."""
+    desc = _lib.make_desc(B, H, N, D, N - 1, True, io, ct, D ** -0.5)
+    assert _lib.bwd_workspace_elems(desc) == B * H * N + B * H * extra
+    bad = _lib.make_desc(B, H, N, 60, N - 1, True, io, ct, 0.125)
+    assert _lib.bwd_workspace_elems(bad) == 0
+
+
 def test_fp32_compute_takes_split_backward(lib):
     desc = _lib.make_desc(8, 12, 197, 64, 196, 1, _lib.F32, _lib.F32, 0.125)
     assert _lib.tile_config(desc, 1)[0] == 1

@@ -1,8 +1,9 @@
 """farope_attn_bwd_noalloc (static device workspace, no allocation) against
 farope_attn_bwd (caller workspace), both called through the C ABI.
 
-Two split-path calls in a row (N > 256, then a smaller D = 128 problem) and
-one one-pass call: the same kernels run with the delta rows in the library's
+Split-path calls in a row (N = 257 at D = 128 with the last row and key
+folded into the dQ tiles, N = 257 at D = 64, then a smaller D = 128 problem)
+and one one-pass call: the same kernels run with the delta rows in the library's
 static array instead of a caller buffer, so dQ, dK and dV must be identical
 bit for bit.  The second call reuses the array the first one left behind.
 """
@@ -35,7 +36,7 @@ def _one(B, H, side, has_cls, D, seed):
     o, lse, res = torch.ops.farope.attn_fwd(q, k, v, rope, n_pos, has_cls, scale, _lib.BF16)
     desc = _lib.make_desc(B, H, N, D, n_pos, has_cls, _lib.BF16, _lib.BF16, scale)
     ref = [torch.empty_like(q) for _ in range(3)]
-    delta = torch.empty(B, H, N, device=DEV, dtype=torch.float32)
+    delta = torch.empty(_lib.bwd_workspace_elems(desc), device=DEV, dtype=torch.float32)
     _lib.attn_bwd(desc, q, k, v, o, do, lse, rope, *ref, delta, res)
     got = [torch.full_like(q, float("nan")) for _ in range(3)]
     _lib.attn_bwd_noalloc(desc, q, k, v, o, do, lse, rope, *got, res)
@@ -47,6 +48,9 @@ def _one(B, H, side, has_cls, D, seed):
 
 
 def test_noalloc_matches_workspace_entry_two_calls():
+    # N = 257, D = 128: the last row and key ride along the dQ tiles (their
+    # partial dK / dV rows go to the workspace past the delta rows)
+    assert _one(2, 3, 16, True, 128, seed=24) == 1
     assert _one(4, 6, 16, True, 64, seed=21) == 1    # split path, N = 257
     assert _one(2, 3, 7, True, 128, seed=22) == 1    # smaller, split path (D = 128)
     assert _one(2, 4, 14, True, 64, seed=23) == 0    # one-pass path (no workspace used)

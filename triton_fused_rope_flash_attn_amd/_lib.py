@@ -31,6 +31,7 @@ EXPORTS = (
     "farope_rope_packed_elems",
     "farope_rope_pack",
     "farope_attn_residual_elems",
+    "farope_attn_bwd_workspace_elems",
     "farope_attn_fwd",
     "farope_attn_bwd_preprocess",
     "farope_attn_bwd_dk_dv",
@@ -68,6 +69,7 @@ _SIGNATURES = {
     "farope_rope_packed_elems": (ctypes.c_size_t, [_I32, _I32]),
     "farope_rope_pack": (ctypes.c_int, [_P, _I64, _I64, _P, _I64, _I64, _I32, _I32, _P, _P]),
     "farope_attn_residual_elems": (ctypes.c_size_t, [_D]),
+    "farope_attn_bwd_workspace_elems": (ctypes.c_size_t, [_D]),
     "farope_attn_fwd": (ctypes.c_int, [_D, _P, _S, _P, _S, _P, _S, _P, _P, _S, _P, _P, _P]),
     "farope_attn_bwd_preprocess": (ctypes.c_int, [_D, _P, _S, _P, _P, _S, _P, _P]),
     "farope_attn_bwd_dk_dv": (
@@ -152,6 +154,11 @@ def rope_pack(cosp: torch.Tensor, sinp: torch.Tensor, out: torch.Tensor) -> None
 def residual_elems(desc: AttnDesc) -> int:
     """Elements of the O-residual buffer the call uses (0: none); see farope_attn_residual_elems."""
     return int(load().farope_attn_residual_elems(ctypes.byref(desc)))
+
+
+def bwd_workspace_elems(desc: AttnDesc) -> int:
+    """fp32 elements of attn_bwd's delta workspace; see farope_attn_bwd_workspace_elems."""
+    return int(load().farope_attn_bwd_workspace_elems(ctypes.byref(desc)))
 
 
 def _ptr(t) -> int | None:

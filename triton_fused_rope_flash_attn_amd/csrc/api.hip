@@ -173,14 +173,39 @@ int dq_pass(BwdParams p, const farope_attn_desc* d, bool write_delta, hipStream_
   return FAROPE_OK;
 }
 
-// dK/dV block kernel (+ the tail keys kernel)
+// dK/dV block kernel (+ the tail keys kernel, or the merge of the dQ tiles'
+// partial rows of the last key when dq_pass wrote them to p.xk_ws)
 int dkdv_pass(BwdParams p, const farope_attn_desc* d, hipStream_t st) {
   const int D = d->head_dim, rows = bwd_dkdv_block_rows(D, d->compute_dtype);
   const int tail = tail_of(p.B * p.H, p.N, rows);
   p.n_blk = main_blocks(p.B * p.H, p.N, rows);
   FAROPE_TRY(launch_rc(launch_bwd_dkdv(p, d->io_dtype, d->compute_dtype, D, st)));
-  if (tail) FAROPE_TRY(launch_rc(launch_bwd_tail_keys(p, d->io_dtype, D, p.N - tail, st)));
+  if (tail && p.xk_ws) {
+    const int nparts = main_blocks(p.B * p.H, p.N, bwd_dq_block_rows(D, d->compute_dtype));
+    FAROPE_TRY(launch_rc(launch_bwd_tail_key_merge(p, d->io_dtype, D, nparts, st)));
+  } else if (tail) {
+    FAROPE_TRY(launch_rc(launch_bwd_tail_keys(p, d->io_dtype, D, p.N - tail, st)));
+  }
   return FAROPE_OK;
+}
+
+// Whether the one-call backward takes the last key's dK / dV from the dQ
+// tiles' partial rows: one row left past both kernels' full blocks, fp16
+// logit operands (vec: K and V allow vector access, as the dQ kernel's
+// folded-row instantiation needs).  The workspace size below assumes vec.
+bool key_from_dq(const farope_attn_desc* d, bool vec) {
+  const int D = d->head_dim, planes = d->batch * d->heads, N = d->seq_len;
+  return tail_of(planes, N, bwd_dq_block_rows(D, d->compute_dtype)) == 1 &&
+         tail_of(planes, N, bwd_dkdv_block_rows(D, d->compute_dtype)) == 1 &&
+         bwd_folds_tail(d->io_dtype, d->compute_dtype, D, vec);
+}
+
+// delta rows, then (key_from_dq) one dK-hat / dV row pair per dQ tile
+int64_t bwd_ws_elems(const farope_attn_desc* d) {
+  const int64_t planes = (int64_t)d->batch * d->heads, rows = planes * d->seq_len;
+  if (bwd_fused(d) || !key_from_dq(d, true)) return rows;
+  const int nb = main_blocks((int)planes, d->seq_len, bwd_dq_block_rows(d->head_dim, d->compute_dtype));
+  return rows + planes * nb * 2 * d->head_dim;
 }
 
 int bwd_impl(const farope_attn_desc* desc, const void* q, const int64_t q_stride[4],
@@ -207,7 +232,7 @@ int bwd_impl(const farope_attn_desc* desc, const void* q, const int64_t q_stride
   const bool fused = bwd_fused(desc);
   if (static_ws) {
     // the split path's delta rows go to this device's static scratch array
-    if ((int64_t)desc->batch * desc->heads * desc->seq_len > kScratchFloats) return FAROPE_ERR_SCRATCH;
+    if (bwd_ws_elems(desc) > kScratchFloats) return FAROPE_ERR_SCRATCH;
     FAROPE_TRY(scratch_ptr(&delta_ws));
   } else if (!fused) {
     FAROPE_TRY(check_ptr(delta_ws, 4));
@@ -237,6 +262,8 @@ int bwd_impl(const farope_attn_desc* desc, const void* q, const int64_t q_stride
     return launch_rc(launch_bwd_fused(p, desc->io_dtype, desc->compute_dtype, st));
   }
   // dQ (and delta, which the dK/dV pass reads for every row) before dK / dV
+  if (key_from_dq(desc, p.vec_k && p.vec_v))
+    p.xk_ws = delta_ws + (int64_t)desc->batch * desc->heads * desc->seq_len;
   FAROPE_TRY(dq_pass(p, desc, true, st));
   return dkdv_pass(p, desc, st);
 }
@@ -300,6 +327,11 @@ int farope_tile_config(const farope_attn_desc* desc, int32_t which, int32_t out[
     out[3] = fu ? 512 : bwd_dkdv_threads(D, desc->compute_dtype);
   }
   return FAROPE_OK;
+}
+
+size_t farope_attn_bwd_workspace_elems(const farope_attn_desc* desc) {
+  if (check_desc(desc) != FAROPE_OK) return 0;
+  return (size_t)bwd_ws_elems(desc);
 }
 
 size_t farope_attn_residual_elems(const farope_attn_desc* desc) {

@@ -118,6 +118,8 @@ bwd_dq_kernel(const BwdParams p) {
   __shared__ __attribute__((aligned(16))) S sXg[XR ? D : 8];
   __shared__ __attribute__((aligned(16))) float sXo[XR ? NW : 1][XR ? D : 4];
   __shared__ float sXd[2];   // delta, LSE2 of the last row
+  // XR with p.xk_ws: per-wave sums of the last key's dK-hat and dV rows
+  __shared__ __attribute__((aligned(16))) float sXk[XR ? NW : 1][XR ? 2 * D : 4];
 
   const int N = p.N;
   const int tile = xcd_remap(block_id(), p.n_wg);
@@ -552,6 +554,108 @@ bwd_dq_kernel(const BwdParams p) {
         for (int r = 0; r < 4; ++r) g4[r] = dqacc[t][d][r] * dq_scale;
         rope_unrotate4(g4, tab, row + shift, D2, 8 * d + 2 * lg);
         store4(dQ + row * p.sdq[2] + (16 * d + 4 * lg) * p.sdq[3], p.sdq[3], p.vec_dq, g4);
+      }
+    }
+  }
+  if constexpr (XR) {
+    if (p.xk_ws) {
+      // The plane's last key (the one key past the dK/dV kernel's full key
+      // blocks): its dK-hat and dV rows summed over this tile's query rows,
+      // from the tile's Q-hat / dO fragments and the key's K-hat / V row,
+      // which the last key block left in LDS (row er).  P and dS as in the
+      // block products (exp2(S - LSE2) clamped to [0, 1]; rows >= N have
+      // zero fragments and add nothing).  Each tile writes one partial row
+      // pair; bwd_tail_key_merge_kernel adds the tiles' rows in a fixed
+      // order.  dK-hat is summed against the fp16 Q-hat (scaled by c2 * fq)
+      // and divided by that scale here.
+      const int er = (N - 1) % KVS;
+      const int ln = opaque(lane);
+      const int lgx = ln >> 4, lrx = ln & 15;
+      float prx[QT], dsx[QT];
+#pragma unroll
+      for (int t = 0; t < QT; ++t) {
+        float sx = 0.f, dpx = 0.f;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const int c0 = 32 * s + 8 * lgx;
+          Raw8<f16> a;
+          a.v = opaque_vec(qf[t][s].v);
+          Raw8<S> b;
+          b.v = opaque_vec(gf[t][s].v);
+          sx = dot8<f16>(a, *reinterpret_cast<const Raw8<f16>*>(&sKf[er * LDK + c0]), sx);
+          dpx = dot8<S>(b, *reinterpret_cast<const Raw8<S>*>(&sV[er * LDK + c0]), dpx);
+        }
+        sx = group4_sum(sx);
+        dpx = group4_sum(dpx);
+        prx[t] = __builtin_amdgcn_fmed3f(fast_exp2(__builtin_fmaf(sx, fsc, -lse2[t])), 0.f, 1.f);
+        dsx[t] = prx[t] * (dpx - dlt[t]);
+      }
+      // each channel's products over the lane's query rows, then the sum over
+      // the 16 query rows of each lane group (DPP within rows of 16)
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        decltype(qf[0][0].v) qv[QT];
+        decltype(gf[0][0].v) gv[QT];
+#pragma unroll
+        for (int t = 0; t < QT; ++t) {
+          qv[t] = opaque_vec(qf[t][s].v);
+          gv[t] = opaque_vec(gf[t][s].v);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float x = 0.f, y = 0.f;
+#pragma unroll
+          for (int t = 0; t < QT; ++t) {
+            x = __builtin_fmaf(dsx[t], (float)qv[t][e], x);
+            y = __builtin_fmaf(prx[t], (float)gv[t][e], y);
+          }
+          x = dpp_sum8(x);
+          y = dpp_sum8(y);
+          x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xF, 0xF, false));
+          y += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y), 0x140, 0xF, 0xF, false));
+          if (lrx == 0) {
+            sXk[wave][32 * s + 8 * lgx + e] = x;
+            sXk[wave][D + 32 * s + 8 * lgx + e] = y;
+          }
+        }
+      }
+      lds_barrier();
+      if (wave == 0) {
+        // the tile's last row (XR item): its own products with the key
+        float px = 0.f, dsxx = 0.f;
+        if (xi) {
+          float s1 = 0.f, d1 = 0.f;
+#pragma unroll
+          for (int i = 0; i < XO; ++i) {
+            const int c = XO * ln + i;
+            s1 = __builtin_fmaf((float)sXq[c], (float)sKf[er * LDK + c], s1);
+            d1 = __builtin_fmaf((float)sXg[c], (float)sV[er * LDK + c], d1);
+          }
+          s1 = dpp_sum8(s1);
+          d1 = dpp_sum8(d1);
+          s1 += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s1), 0x140, 0xF, 0xF, false));
+          d1 += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(d1), 0x140, 0xF, 0xF, false));
+          s1 = group4_sum(s1);
+          d1 = group4_sum(d1);
+          px = __builtin_amdgcn_fmed3f(fast_exp2(__builtin_fmaf(s1, fsc, -sXd[1])), 0.f, 1.f);
+          dsxx = px * (d1 - sXd[0]);
+        }
+        const float iq = 1.f / (p.scale_log2 * fq);
+        float* ws = p.xk_ws + ((int64_t)plane * p.n_blk + qblk) * (2 * D);
+#pragma unroll
+        for (int m = 0; m < 2 * D / 64; ++m) {
+          const int j = ln + 64 * m;
+          float x = 0.f;
+#pragma unroll
+          for (int w = 0; w < NW; ++w) x += sXk[w][j];
+          if (j < D) {
+            if (xi) x = __builtin_fmaf(dsxx, (float)sXq[j], x);
+            x *= iq;
+          } else {
+            if (xi) x = __builtin_fmaf(px, (float)sXg[j - D], x);
+          }
+          ws[j] = x;
+        }
       }
     }
   }

@@ -582,6 +582,14 @@ __device__ __forceinline__ float opaque(float x) {
   return x;
 }
 
+// The same for a 16-byte register vector (an MFMA operand fragment): values
+// computed from it after a loop are formed there, not kept from before it.
+template <typename V>
+__device__ __forceinline__ V opaque_vec(V x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 // Workgroup barrier that orders LDS traffic only.  The waves of these kernels
 // exchange data through LDS alone, so the barrier waits for outstanding LDS
 // operations (lgkmcnt) but not for global loads and stores (vmcnt): prefetches

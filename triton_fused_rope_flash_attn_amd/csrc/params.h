@@ -48,6 +48,8 @@ struct BwdParams {
   int n_blk;           // q blocks (dq kernel) or kv blocks (dk/dv kernel) per plane
   int n_wg;            // workgroups of the launch (set by the launcher)
   int x_rows;          // 1: the dQ block kernel also computes row N - 1 (bwd_folds_tail)
+  float* xk_ws;        // non-null: the dQ kernel's tiles write their partial dK-hat / dV
+                       // rows of key N - 1 here ([planes][n_blk][2][D] fp32)
 };
 
 // Launch shapes picked by the tile table (api.hip).
@@ -78,6 +80,9 @@ hipError_t launch_fwd_tail(const FwdParams& p, int io, int D, int row0, hipStrea
 hipError_t launch_bwd_tail_rows(const BwdParams& p, int io, int D, int row0, bool write_delta,
                                 hipStream_t st);
 hipError_t launch_bwd_tail_keys(const BwdParams& p, int io, int D, int key0, hipStream_t st);
+// Key N - 1 from the dQ kernel's per-tile partial rows (p.xk_ws, nparts per
+// plane) instead of launch_bwd_tail_keys; D = 128 or 256, 16-bit I/O.
+hipError_t launch_bwd_tail_key_merge(const BwdParams& p, int io, int D, int nparts, hipStream_t st);
 // Whether the forward block kernel computes a single tail row itself
 // (FwdParams::x_rows = 1) instead of launch_fwd_tail: fp16 logit operands with
 // vector access (vec: every tensor of the call allows it).

@@ -312,6 +312,31 @@ __global__ void __launch_bounds__(kTailThreads) bwd_tail_keys_kernel(const BwdPa
   }
 }
 
+// The plane's last key when the dQ kernel summed its dK-hat / dV rows per
+// query tile (p.xk_ws: nparts row pairs per plane, dK-hat then dV): the
+// tiles' rows added in order, dK-hat scaled and rotated back, both stored.
+// One workgroup per plane, D/4 threads of 4 channels.
+template <typename IO, int D>
+__global__ void __launch_bounds__(D / 4) bwd_tail_key_merge_kernel(const BwdParams p, int nparts) {
+  const int plane = block_id(), tid = thread_id();
+  const int N = p.N, kc = N - 1, shift = 1 - p.has_cls;
+  const float* w = p.xk_ws + (int64_t)plane * nparts * (2 * D);
+  float xk[4] = {}, xv[4] = {};
+  for (int b = 0; b < nparts; ++b)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      xk[e] += w[b * 2 * D + 4 * tid + e];
+      xv[e] += w[b * 2 * D + D + 4 * tid + e];
+    }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) xk[e] *= p.scale;
+  rope_unrotate4(xk, p.rope, kc + shift, D / 2, 2 * tid);
+  IO* DK = const_cast<IO*>(plane_row<IO>(p.dk, p.sdk, plane, p.H, kc));
+  IO* DV = const_cast<IO*>(plane_row<IO>(p.dv, p.sdv, plane, p.H, kc));
+  store4(DK + 4 * tid * p.sdk[3], p.sdk[3], p.vec_dk, xk);
+  store4(DV + 4 * tid * p.sdv[3], p.sdv[3], p.vec_dv, xv);
+}
+
 template <typename IO, bool VEC>
 hipError_t fwd_tail_v(const FwdParams& p, int D, int row0, hipStream_t st) {
   const dim3 grid(p.B * p.H * (p.N - row0)), block(kTailThreads);
@@ -393,6 +418,21 @@ hipError_t launch_bwd_tail_rows(const BwdParams& p, int io, int D, int row0, boo
     case DT_F16: return rows_tail_d<f16>(p, D, row0, write_delta, st);
     default: return rows_tail_d<float>(p, D, row0, write_delta, st);
   }
+}
+
+hipError_t launch_bwd_tail_key_merge(const BwdParams& p, int io, int D, int nparts, hipStream_t st) {
+  const dim3 grid(p.B * p.H);
+  if (io != DT_BF16 && io != DT_F16) return hipErrorInvalidValue;
+  if (D == 128) {
+    if (io == DT_BF16) hipLaunchKernelGGL((bwd_tail_key_merge_kernel<bf16, 128>), grid, dim3(32), 0, st, p, nparts);
+    else hipLaunchKernelGGL((bwd_tail_key_merge_kernel<f16, 128>), grid, dim3(32), 0, st, p, nparts);
+  } else if (D == 256) {
+    if (io == DT_BF16) hipLaunchKernelGGL((bwd_tail_key_merge_kernel<bf16, 256>), grid, dim3(64), 0, st, p, nparts);
+    else hipLaunchKernelGGL((bwd_tail_key_merge_kernel<f16, 256>), grid, dim3(64), 0, st, p, nparts);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_bwd_tail_keys(const BwdParams& p, int io, int D, int key0, hipStream_t st) {
