@@ -42,7 +42,7 @@ typedef enum farope_status {
   FAROPE_ERR_SHAPE = 6,       /* batch/heads not positive or sizes overflow */
   FAROPE_ERR_LAUNCH = 7,      /* the HIP runtime rejected a kernel launch */
   FAROPE_ERR_ALIGN = 8,       /* a pointer is not aligned to its element size */
-  FAROPE_ERR_SCRATCH = 9      /* batch*heads*seq_len > FAROPE_NOALLOC_MAX_ROWS (noalloc entry) */
+  FAROPE_ERR_SCRATCH = 9      /* workspace elems > FAROPE_NOALLOC_MAX_ROWS (noalloc entry) */
 } farope_status;
 
 /* Rows (batch * heads * seq_len) the static workspace of
@@ -175,10 +175,11 @@ int farope_attn_bwd(const farope_attn_desc* desc,
  * farope_attn_bwd without the caller workspace: no counterpart in the
  * reference.  For callers that cannot allocate device memory (code under HIP
  * graph capture, serving loops, harnesses that forbid hipMalloc).  The split
- * path's delta rows live in a static device array of FAROPE_NOALLOC_MAX_ROWS
- * fp32 values that the library holds on every device it runs on until the
- * process ends; larger calls return FAROPE_ERR_SCRATCH before anything is
- * launched.  Allocates nothing.  Calls on one device share that array, so
+ * path's workspace (farope_attn_bwd_workspace_elems: the delta rows, and the
+ * partial rows of a lone last key) lives in a static device array of
+ * FAROPE_NOALLOC_MAX_ROWS fp32 values that the library holds on every device
+ * it runs on until the process ends; calls that need more return
+ * FAROPE_ERR_SCRATCH before anything is launched.  Allocates nothing.  Calls on one device share that array, so
  * calls that overlap on one device (concurrent streams or threads) race;
  * calls ordered on one stream do not.  The current device must be the one
  * holding the tensors.

@@ -12,7 +12,9 @@
 using namespace farope;
 
 // Workspace of farope_attn_bwd_noalloc: the split backward's delta rows (fp32,
-// one per query row of the call, B*H*N <= FAROPE_NOALLOC_MAX_ROWS = 16 MiB).
+// one per query row of the call) and, for a lone last key, the dQ tiles'
+// partial dK / dV rows after them (bwd_ws_elems <= FAROPE_NOALLOC_MAX_ROWS,
+// 16 MiB).
 // The runtime gives every device its own copy when it loads the code object,
 // held until the process ends.  In host code this name is only a handle for
 // hipGetSymbolAddress: kernels receive the device address it returns.
@@ -287,7 +289,7 @@ const char* farope_strerror(int status) {
     case FAROPE_ERR_LAUNCH: return "farope: HIP kernel launch failed";
     case FAROPE_ERR_ALIGN: return "farope: pointer not aligned to its element size";
     case FAROPE_ERR_SCRATCH:
-      return "farope: batch*heads*seq_len exceeds the static workspace of farope_attn_bwd_noalloc "
+      return "farope: the backward workspace (farope_attn_bwd_workspace_elems) exceeds the static workspace of farope_attn_bwd_noalloc "
              "(FAROPE_NOALLOC_MAX_ROWS = 4194304); use farope_attn_bwd with a caller workspace";
     default: return "farope: unknown status";
   }
