@@ -498,6 +498,11 @@ fwd_kernel(const FwdParams p) {
   };
 
   float m_run[QT], l_run[QT], m_thr[QT];
+  // Pipelined chunks (kPipe): the logits accumulators of a block start at
+  // -mb (mb = m_run once it is finite, else 0), so the MFMAs deliver
+  // S - m_run and P = exp2(acc) needs no subtraction; m_thr then holds the
+  // threshold relative to mb.
+  float mb[QT];
   f32x4 oacc[QT][DT];
 
   // The 32-key blocks of a KV chunk run as a software pipeline over all QT
@@ -543,7 +548,7 @@ fwd_kernel(const FwdParams p) {
   // S^T = K-hat Q-hat^T for 32 keys (each K-hat fragment feeds QT MFMAs)
   auto logits = [&](const KFr& kf, SAcc& sa) __attribute__((always_inline)) {
 #pragma unroll
-    for (int t = 0; t < QT; ++t) sa[t][0] = sa[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < QT; ++t) sa[t][0] = sa[t][1] = f32x4{-mb[t], -mb[t], -mb[t], -mb[t]};
     if constexpr (!FS) {   // (the pipelined chunk runs without fp16 operands)
 #pragma unroll
       for (int s = 0; s < KS; ++s)
@@ -557,8 +562,10 @@ fwd_kernel(const FwdParams p) {
   // block for its query row.  MASKED: keys e >= lim get probability 0.
   // The running max only has to bound the exponent: O and the row sum are
   // rescaled (group max, times 2^(m_old - m_new)) only when some lane's own
-  // max exceeds m_thr = m_run + slack (logits, m_run and m_thr are all in
-  // log2 units through the pre-scaled K-hat).
+  // max exceeds m_run + slack.  The block's values arrive as logits minus
+  // m_run (accumulators seeded with -mb, all in log2 units through the
+  // pre-scaled K-hat), so the test is against m_thr = slack (-inf before
+  // the first block) and P is exp2 of the values themselves.
   //
   // The common case has no branch: soft() computes P with the current
   // running max and reports whether any row crossed its threshold; only then
@@ -578,11 +585,12 @@ fwd_kernel(const FwdParams p) {
   auto max8 = [](const float (&sv)[8]) __attribute__((always_inline)) {
     return fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
   };
+  // sv: logits minus the running max (the seeded accumulators)
   auto probs = [&](const float (&sv)[8], int t, Frag& pft) __attribute__((always_inline)) {
     float pv8[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      pv8[e] = fast_exp2(sv[e] - m_run[t]);
+      pv8[e] = fast_exp2(sv[e]);
       l_run[t] += pv8[e];
     }
     pft = C::make(pv8);
@@ -599,25 +607,37 @@ fwd_kernel(const FwdParams p) {
     }
     return need;
   };
-  auto fixup = [&](auto maskc, const SAcc& sa, int lim, Frag (&pf)[QT], const float (&lkeep)[QT]) __attribute__((always_inline)) {
+  // The new base also applies to a block whose logits are already issued
+  // (pend): its accumulators are shifted by the change.
+  auto fixup = [&](auto maskc, const SAcc& sa, int lim, Frag (&pf)[QT], const float (&lkeep)[QT],
+                   SAcc* pend) __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
       float sv[8];
       block_vals(maskc, sa, t, lim, sv);
-      const float mx = group4_max(max8(sv));
+      const float mx = group4_max(max8(sv)) + mb[t];
       const float mnew = fmaxf(m_run[t], mx);
       const float alpha = fast_exp2(m_run[t] - mnew);
       l_run[t] = lkeep[t] * alpha;
 #pragma unroll
       for (int d = 0; d < DT; ++d) oacc[t][d] *= alpha;
       m_run[t] = mnew;
-      m_thr[t] = mnew + kRescaleSlack;
+      const float mbn = mnew == -INFINITY ? mb[t] : mnew;
+      const float shift = mb[t] - mbn;
+      mb[t] = mbn;
+      m_thr[t] = kRescaleSlack;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sv[e] += shift;
       probs(sv, t, pf[t]);
+      if (pend) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) (*pend)[t][h] += shift;
+      }
     }
   };
-  auto softmax = [&](auto maskc, const SAcc& sa, int lim, Frag (&pf)[QT]) __attribute__((always_inline)) {
+  auto softmax = [&](auto maskc, const SAcc& sa, int lim, Frag (&pf)[QT], SAcc* pend) __attribute__((always_inline)) {
     float lkeep[QT];
-    if (soft(maskc, sa, lim, pf, lkeep)) fixup(maskc, sa, lim, pf, lkeep);
+    if (soft(maskc, sa, lim, pf, lkeep)) fixup(maskc, sa, lim, pf, lkeep, pend);
   };
   // O^T += V^T P^T (each V^T fragment feeds QT MFMAs)
   auto out_mma = [&](const VFr& vf, const Frag (&pf)[QT]) __attribute__((always_inline)) {
@@ -655,15 +675,15 @@ fwd_kernel(const FwdParams p) {
       logits(kn, nxt);
       load_k(cK, min(j + 2, nb - 1), kfree);
       load_v(cV, j, vf);
-      softmax(std::false_type{}, cur, 8, pf);
+      softmax(std::false_type{}, cur, 8, pf, &nxt);
       out_mma(vf, pf);
     };
     auto last = [&](int j, const SAcc& cur) __attribute__((always_inline)) {
       load_v(cV, j, vf);
       if (nkeys & 31)
-        softmax(std::true_type{}, cur, N - (kvb + 32 * j + 8 * lg), pf);
+        softmax(std::true_type{}, cur, N - (kvb + 32 * j + 8 * lg), pf, nullptr);
       else
-        softmax(std::false_type{}, cur, 8, pf);
+        softmax(std::false_type{}, cur, 8, pf, nullptr);
       out_mma(vf, pf);
     };
     int j = 0;
@@ -674,7 +694,7 @@ fwd_kernel(const FwdParams p) {
     if (j + 1 < nb) {
       logits(kb, s1);
       load_v(cV, j, vf);
-      softmax(std::false_type{}, s0, 8, pf);
+      softmax(std::false_type{}, s0, 8, pf, &s1);
       out_mma(vf, pf);
       last(j + 1, s1);
     } else {
@@ -913,6 +933,7 @@ fwd_kernel(const FwdParams p) {
       nt += (qb * NW * QT + t * NW + wave) * 16 < N;
       m_run[t] = -INFINITY;
       m_thr[t] = -INFINITY;
+      mb[t] = 0.f;
       l_run[t] = 0.f;
 #pragma unroll
       for (int d = 0; d < DT; ++d) oacc[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
