@@ -81,23 +81,29 @@ def test_tile_table(lib, N, D, has_cls, fwd_items, bwd_var):
 
 
 @pytest.mark.parametrize(
-    "B,H,N,D,io,ct,extra",
+    "B,H,N,D,io,ct,extra,hat",
     [
-        (32, 12, 1025, 128, _lib.BF16, _lib.BF16, 4 * 2 * 128),   # HiRes: 4 dQ tiles per plane
-        (2, 3, 257, 256, _lib.BF16, _lib.BF16, 4 * 2 * 256),      # 64-row dQ tiles
-        (2, 3, 257, 128, _lib.F16, _lib.BF16, 1 * 2 * 128),       # fp16 I/O, bf16 compute
-        (256, 12, 197, 64, _lib.BF16, _lib.BF16, 0),              # one-pass backward
-        (2, 3, 257, 64, _lib.BF16, _lib.BF16, 0),                 # no fp16 logits at D = 64
-        (2, 3, 257, 128, _lib.F16, _lib.F16, 0),                  # fp16 compute
-        (2, 3, 1100, 128, _lib.BF16, _lib.BF16, 0),               # 76 rows past the blocks
-        (2, 3, 3970, 128, _lib.BF16, _lib.BF16, 0),               # dQ blocks leave 130 rows
+        (32, 12, 1025, 128, _lib.BF16, _lib.BF16, 4 * 2 * 128, True),   # HiRes: 4 dQ tiles per plane
+        (2, 3, 257, 256, _lib.BF16, _lib.BF16, 4 * 2 * 256, True),      # 64-row dQ tiles
+        (2, 3, 257, 128, _lib.F16, _lib.BF16, 1 * 2 * 128, True),       # fp16 I/O, bf16 compute
+        (256, 12, 197, 64, _lib.BF16, _lib.BF16, 0, False),             # one-pass backward
+        (2, 3, 257, 64, _lib.BF16, _lib.BF16, 0, False),                # no fp16 logits at D = 64
+        (2, 3, 257, 128, _lib.F16, _lib.F16, 0, False),                 # fp16 compute
+        (2, 3, 1100, 128, _lib.BF16, _lib.BF16, 0, True),               # 76 rows past the blocks
+        (2, 3, 3970, 128, _lib.BF16, _lib.BF16, 0, True),               # dQ blocks leave 130 rows
+        (1, 2, 3844, 128, _lib.BF16, _lib.BF16, 0, False),              # 4 tail rows: tail kernel
     ],
 )
-def test_bwd_workspace_elems(lib, B, H, N, D, io, ct, extra):
-    """delta rows, plus one partial dK / dV row pair per dQ tile when the plane's
-    lone last key is summed by those tiles (fp16 logits, N = 1 + k * 256)."""
+def test_bwd_workspace_elems(lib, B, H, N, D, io, ct, extra, hat):
+    """delta rows; one partial dK / dV row pair per dQ tile when the plane's lone
+    last key is summed by those tiles (fp16 logits, N = 1 + k * 256); then, from a
+    64-float boundary, the dQ pass's fp16 Q-hat rows for the dK/dV pass (fp16
+    logits, every row in a dQ tile)."""
     desc = _lib.make_desc(B, H, N, D, N - 1, True, io, ct, D ** -0.5)
-    assert _lib.bwd_workspace_elems(desc) == B * H * N + B * H * extra
+    n = B * H * N + B * H * extra
+    if hat:
+        n = (n + 63) // 64 * 64 + B * H * N * D // 2
+    assert _lib.bwd_workspace_elems(desc) == n
     bad = _lib.make_desc(B, H, N, 60, N - 1, True, io, ct, 0.125)
     assert _lib.bwd_workspace_elems(bad) == 0
 

@@ -202,13 +202,38 @@ bool key_from_dq(const farope_attn_desc* d, bool vec) {
          bwd_folds_tail(d->io_dtype, d->compute_dtype, D, vec);
 }
 
-// delta rows, then (key_from_dq) one dK-hat / dV row pair per dQ tile
-int64_t bwd_ws_elems(const farope_attn_desc* d) {
-  const int64_t planes = (int64_t)d->batch * d->heads, rows = planes * d->seq_len;
-  if (bwd_fused(d) || !key_from_dq(d, true)) return rows;
-  const int nb = main_blocks((int)planes, d->seq_len, bwd_dq_block_rows(d->head_dim, d->compute_dtype));
-  return rows + planes * nb * 2 * d->head_dim;
+// Whether the dQ kernel can hand its rotated Q rows to the dK/dV kernel
+// (fp16 logit operands; every row is a dQ-tile row: no tail, or the folded
+// one).  The dK/dV kernel then also needs vector access to dO (checked at
+// the call).
+bool qhat_possible(const farope_attn_desc* d) {
+  const int D = d->head_dim, planes = d->batch * d->heads, N = d->seq_len;
+  if (bwd_fused(d) || d->io_dtype == FAROPE_F32 || !f16_logits(d->compute_dtype, D)) return false;
+  const int t = tail_of(planes, N, bwd_dq_block_rows(D, d->compute_dtype));
+  return t == 0 || (t == 1 && bwd_folds_tail(d->io_dtype, d->compute_dtype, D, true));
 }
+
+// Workspace of the split backward, in fp32 elements: the delta rows, then
+// (key_from_dq) one dK-hat / dV row pair per dQ tile, then (with_hat and
+// qhat_possible, from a 256-byte boundary) the rotated Q rows in fp16.
+struct BwdWs {
+  int64_t keys, hat, total;   // offsets of the key rows and of the rotated rows; size
+};
+BwdWs bwd_ws(const farope_attn_desc* d, bool with_hat) {
+  const int64_t planes = (int64_t)d->batch * d->heads, rows = planes * d->seq_len;
+  BwdWs w{rows, 0, rows};
+  if (bwd_fused(d)) return w;
+  if (key_from_dq(d, true)) {
+    const int nb = main_blocks((int)planes, d->seq_len, bwd_dq_block_rows(d->head_dim, d->compute_dtype));
+    w.total += planes * nb * 2 * d->head_dim;
+  }
+  if (with_hat && qhat_possible(d)) {
+    w.hat = (w.total + 63) & ~int64_t(63);
+    w.total = w.hat + rows * d->head_dim / 2;   // [planes][N][D] fp16
+  }
+  return w;
+}
+int64_t bwd_ws_elems(const farope_attn_desc* d) { return bwd_ws(d, false).total; }
 
 int bwd_impl(const farope_attn_desc* desc, const void* q, const int64_t q_stride[4],
              const void* k, const int64_t k_stride[4], const void* v, const int64_t v_stride[4],
@@ -266,6 +291,18 @@ int bwd_impl(const farope_attn_desc* desc, const void* q, const int64_t q_stride
   // dQ (and delta, which the dK/dV pass reads for every row) before dK / dV
   if (key_from_dq(desc, p.vec_k && p.vec_v))
     p.xk_ws = delta_ws + (int64_t)desc->batch * desc->heads * desc->seq_len;
+  // the rotated Q rows go to the workspace too: always for a caller
+  // workspace (sized by farope_attn_bwd_workspace_elems), for the static one
+  // when they fit
+  if (qhat_possible(desc) && p.vec_q && p.vec_do &&
+      (!static_ws || bwd_ws(desc, true).total <= kScratchFloats)) {
+    const BwdWs w = bwd_ws(desc, true);
+    const int tq = tail_of(p.B * p.H, p.N, bwd_dq_block_rows(D, desc->compute_dtype));
+    float* hat = delta_ws + w.hat;
+    if ((tq == 0 || bwd_folds_tail(desc->io_dtype, desc->compute_dtype, D, p.vec_k && p.vec_v)) &&
+        reinterpret_cast<uintptr_t>(hat) % 16 == 0)
+      p.qhat_f = hat;
+  }
   FAROPE_TRY(dq_pass(p, desc, true, st));
   return dkdv_pass(p, desc, st);
 }
@@ -333,7 +370,7 @@ int farope_tile_config(const farope_attn_desc* desc, int32_t which, int32_t out[
 
 size_t farope_attn_bwd_workspace_elems(const farope_attn_desc* desc) {
   if (check_desc(desc) != FAROPE_OK) return 0;
-  return (size_t)bwd_ws_elems(desc);
+  return (size_t)bwd_ws(desc, true).total;
 }
 
 size_t farope_attn_residual_elems(const farope_attn_desc* desc) {

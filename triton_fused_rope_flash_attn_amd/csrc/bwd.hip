@@ -217,6 +217,8 @@ bwd_dq_kernel(const BwdParams p) {
       for (int e = 0; e < 8; ++e) x[e] *= qs;
       amax_q = amax8(amax_q, x);
       *reinterpret_cast<f16x8*>(&sXq[c0]) = to_f16x8(x);
+      if (p.qhat_f != nullptr && !rescaled)   // (see the tile rows' store below)
+        *reinterpret_cast<f16x8*>(static_cast<f16*>(p.qhat_f) + (prow + row) * D + c0) = to_f16x8(x);
       load8(G + row * p.sdo[2] + c0 * p.sdo[3], p.sdo[3], p.vec_do, g);
       C::put8(&sXg[c0], g);
       float dsum;
@@ -337,6 +339,23 @@ bwd_dq_kernel(const BwdParams p) {
   };
 
   prefetch(0);
+  if constexpr (FS) {
+    // First pass (fq = 1): the tile's fp16 Q-hat rows (scaled by c2) for the
+    // dK/dV kernel, which then stages them instead of rotating Q again.
+    // Issued after the first key block's loads, so that waiting for those
+    // does not also wait for these stores.
+    if (p.qhat_f != nullptr && !rescaled) {
+#pragma unroll
+      for (int t = 0; t < QT; ++t) {
+        const int row = qrow[t];
+        if (row < N) {
+#pragma unroll
+          for (int s = 0; s < KS; ++s)
+            *reinterpret_cast<f16x8*>(static_cast<f16*>(p.qhat_f) + (prow + row) * D + 32 * s + 8 * lg) = qf[t][s].v;
+        }
+      }
+    }
+  }
   for (int kvb = 0; kvb < N; kvb += KVS) {
     const int rows = min(KVS, round_up32(N - kvb));
     if (kvb > 0) lds_barrier();
@@ -675,7 +694,13 @@ bwd_dq_kernel(const BwdParams p) {
 // Q-hat tile next to the bf16 one the dK product reads; K-hat in registers),
 // and dK-hat^T += Q-hat^T dS_hi + Q-hat^T dS_lo.  A tile whose Q-hat or K-hat
 // reaches 2^12 is computed again with scaled logit operands.
-template <typename IO, int CT, int D, int NW, int KT, int QS, bool VEC, bool FS>
+// HAT (FS, VEC): the stage's Q-hat rows come rotated from the dQ kernel's
+// first pass (p.qhat_f: fp16 of Q-hat * c2), so a stage loads one 16-byte
+// row segment per unit instead of the Q row and its 32 bytes of table; the
+// bf16 Q-hat of the dK product is that value divided by c2.  A pass whose
+// fp16 rows overflowed (inf) or underflowed (max below 2^-10) rotates Q
+// again (raw), and a rescaled pass does too.
+template <typename IO, int CT, int D, int NW, int KT, int QS, bool VEC, bool FS, bool HAT>
 __global__ void __launch_bounds__(NW * 64)
 bwd_dkdv_kernel(const BwdParams p) {
   using C = Comp<CT>;
@@ -724,6 +749,10 @@ bwd_dkdv_kernel(const BwdParams p) {
   float amax_q = 0.f, amax_k = 0.f;
   float fq = 1.f, fk = 1.f, fsc = 1.f;
   bool rescaled = false;
+  // HAT: a pass that rotates Q itself because the dQ kernel's fp16 rows hid
+  // the operand range
+  bool raw = false;
+  const float ic2 = 1.f / p.scale_log2;
   for (;;) {   // one pass, or two when FS rescales
   // (FS: the lane index is opaque to the compiler, so that no lane-dependent
   // address of the pass is hoisted out of this loop to hold registers)
@@ -800,25 +829,44 @@ bwd_dkdv_kernel(const BwdParams p) {
   constexpr unsigned ES = sizeof(IO);
   static_assert(!VEC || (QS * CPR) % NT == 0, "every thread stages whole units");
   static_assert(!VEC || QS <= NT, "one thread per staged LSE / delta");
-  Raw8<IO> pq[VEC ? ITER : 1], pg[VEC ? ITER : 1];
-  f32x4 pt[VEC ? ITER : 1][2];
+  static_assert(!HAT || (FS && VEC), "rotated rows come with fp16 logits and vector access");
+  Raw8<IO> pq[VEC && !HAT ? ITER : 1], pg[VEC ? ITER : 1];
+  f32x4 pt[VEC && !HAT ? ITER : 1][2];
+  Raw8<f16> pqf[HAT ? ITER : 1];
   float pl = 0.f, pd = 0.f;
   auto prefetch = [&](int qb) __attribute__((always_inline)) {
     if constexpr (VEC) {
-      const auto rQ = make_rsrc(Q, (unsigned)(((int64_t)(N - 1) * p.sq[2] + D) * ES));
       const auto rG = make_rsrc(G, (unsigned)(((int64_t)(N - 1) * p.sdo[2] + D) * ES));
+      if constexpr (HAT) {
+        if (!rescaled && !raw) {   // (otherwise commit rotates Q itself)
+          const auto rF = make_rsrc(static_cast<const f16*>(p.qhat_f) + prow * D, (unsigned)(N * D * 2));
+#pragma unroll
+          for (int it = 0; it < ITER; ++it) {
+            const int c = tid + it * NT;
+            const int r = c / CPR, cc = c - r * CPR;
+            pqf[it] = buf_load8<f16>(rF, (unsigned)((r * D + 8 * cc) * 2), (unsigned)(qb * D * 2));
+          }
+        }
+      } else {
+        const auto rQ = make_rsrc(Q, (unsigned)(((int64_t)(N - 1) * p.sq[2] + D) * ES));
+#pragma unroll
+        for (int it = 0; it < ITER; ++it) {
+          const int c = tid + it * NT;
+          const int r = c / CPR, cc = c - r * CPR;
+          pq[it] = buf_load8<IO>(rQ, (unsigned)((r * (int)p.sq[2] + 8 * cc) * (int)ES),
+                                 (unsigned)(qb * (int)p.sq[2] * (int)ES));
+          // rows >= N are zero; any table row serves them
+          const f32x4* t = reinterpret_cast<const f32x4*>(tab + ((int64_t)(min(qb + r, N - 1) + shift) * D2 + 4 * cc) * 2);
+          pt[it][0] = t[0];
+          pt[it][1] = t[1];
+        }
+      }
 #pragma unroll
       for (int it = 0; it < ITER; ++it) {
         const int c = tid + it * NT;
         const int r = c / CPR, cc = c - r * CPR;
-        pq[it] = buf_load8<IO>(rQ, (unsigned)((r * (int)p.sq[2] + 8 * cc) * (int)ES),
-                               (unsigned)(qb * (int)p.sq[2] * (int)ES));
         pg[it] = buf_load8<IO>(rG, (unsigned)((r * (int)p.sdo[2] + 8 * cc) * (int)ES),
                                (unsigned)(qb * (int)p.sdo[2] * (int)ES));
-        // rows >= N are zero; any table row serves them
-        const f32x4* t = reinterpret_cast<const f32x4*>(tab + ((int64_t)(min(qb + r, N - 1) + shift) * D2 + 4 * cc) * 2);
-        pt[it][0] = t[0];
-        pt[it][1] = t[1];
       }
       if (tid < QS) {   // wave-uniform (QS is a multiple of 64)
         const auto rl = make_rsrc(p.lse + prow, (unsigned)N * 4u);
@@ -835,12 +883,37 @@ bwd_dkdv_kernel(const BwdParams p) {
         const int c = tid + it * NT;
         const int r = c / CPR, cc = c - r * CPR;
         float xq[8], xg[8];
-        unpack8(pq[it], xq);
         unpack8(pg[it], xg);
-        const float cs[8] = {pt[it][0][0], pt[it][0][1], pt[it][0][2], pt[it][0][3],
-                             pt[it][1][0], pt[it][1][1], pt[it][1][2], pt[it][1][3]};
-        rope_rotate8(xq, cs);
-        put_qhat(qrow(r) * LDQ + 8 * cc, xq);
+        if constexpr (HAT) {
+          if (!rescaled && !raw) {
+            // the dQ pass's rotated rows (rows >= N read 0)
+            *reinterpret_cast<f16x8*>(&sQf[qrow(r) * LDQ + 8 * cc]) = pqf[it].v;
+            float xf[8];
+            unpack8(pqf[it], xf);
+            amax_q = opaque(amax8(amax_q, xf));
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xf[e] *= ic2;
+            C::put8(&sQ[qrow(r) * LDQ + 8 * cc], xf);
+          } else {
+            const int gr = qb + r;
+            if (gr < N) {
+              float cs[8];
+              load8(Q + gr * p.sq[2] + 8 * cc * p.sq[3], p.sq[3], true, xq);
+              rope_load4(tab, gr + shift, D2, 4 * cc, cs);
+              rope_rotate8(xq, cs);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) xq[e] = 0.f;
+            }
+            put_qhat(qrow(r) * LDQ + 8 * cc, xq);
+          }
+        } else {
+          unpack8(pq[it], xq);
+          const float cs[8] = {pt[it][0][0], pt[it][0][1], pt[it][0][2], pt[it][0][3],
+                               pt[it][1][0], pt[it][1][1], pt[it][1][2], pt[it][1][3]};
+          rope_rotate8(xq, cs);
+          put_qhat(qrow(r) * LDQ + 8 * cc, xq);
+        }
         C::put8(&sG[qrow(r) * LDQ + 8 * cc], xg);
         if constexpr (!TR) {
 #pragma unroll
@@ -1019,6 +1092,15 @@ bwd_dkdv_kernel(const BwdParams p) {
     }
     const unsigned eq = __builtin_amdgcn_readfirstlane(rq) >> 23;
     const unsigned ek = __builtin_amdgcn_readfirstlane(rk) >> 23;
+    if constexpr (HAT) {
+      // fp16 rows of the dQ pass that overflowed (inf) or are all below
+      // 2^-10 (their bf16 Q-hat would lose precision): the same pass from Q
+      if (!raw && !rescaled && (eq >= 255u || eq < 117u)) {
+        raw = true;
+        amax_q = amax_k = 0.f;
+        continue;
+      }
+    }
     if (!rescaled && (eq >= kF16ExpLimit || ek >= kF16ExpLimit)) {
       rescaled = true;
       fq = f16_fit(eq);
@@ -1206,12 +1288,19 @@ static hipError_t dkdv_launch(const BwdParams& p0, hipStream_t st) {
   // (fp32 compute has no registers to spare for the prefetch)
   if constexpr (CT != DT_F32) {
     if (p.vec_q && p.vec_do) {
-      hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS, true, FS>), dim3(grid),
+      if constexpr (FS) {
+        if (p.qhat_f) {
+          hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS, true, FS, true>),
+                             dim3(grid), dim3(SH::KV_NW * 64), 0, st, p);
+          return hipGetLastError();
+        }
+      }
+      hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS, true, FS, false>), dim3(grid),
                          dim3(SH::KV_NW * 64), 0, st, p);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS, false, FS>), dim3(grid),
+  hipLaunchKernelGGL((bwd_dkdv_kernel<IO, CT, D, SH::KV_NW, SH::KV_KT, SH::KV_QS, false, FS, false>), dim3(grid),
                      dim3(SH::KV_NW * 64), 0, st, p);
   return hipGetLastError();
 }

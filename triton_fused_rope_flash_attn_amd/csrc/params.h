@@ -50,6 +50,9 @@ struct BwdParams {
   int x_rows;          // 1: the dQ block kernel also computes row N - 1 (bwd_folds_tail)
   float* xk_ws;        // non-null: the dQ kernel's tiles write their partial dK-hat / dV
                        // rows of key N - 1 here ([planes][n_blk][2][D] fp32)
+  void* qhat_f;        // non-null (fp16 logits): fp16 of Q-hat * scale * log2(e),
+                       // [planes][N][D], written by the dQ kernel's first pass and
+                       // staged by the dK/dV kernel
 };
 
 // Launch shapes picked by the tile table (api.hip).
