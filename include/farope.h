@@ -102,8 +102,11 @@ size_t farope_attn_residual_elems(const farope_attn_desc* desc);
  * is the only one past the dK/dV kernel's full key blocks at fp16-logit
  * shapes (bf16 compute, head_dim 128 or 256, N = 1 + a multiple of 256), one
  * partial dK / dV row pair per dQ tile: those tiles add that key's products
- * over their own query rows instead of a kernel that re-reads the plane.
- * 0 on an invalid descriptor.
+ * over their own query rows instead of a kernel that re-reads the plane;
+ * then, at those fp16-logit shapes whenever every row lies in a dQ tile,
+ * batch * heads * seq_len * head_dim fp16 values (from a 256-byte boundary):
+ * the dQ pass's rotated Q rows, which the dK/dV pass stages instead of
+ * rotating Q again for every key tile.  0 on an invalid descriptor.
  */
 size_t farope_attn_bwd_workspace_elems(const farope_attn_desc* desc);
 
@@ -175,11 +178,13 @@ int farope_attn_bwd(const farope_attn_desc* desc,
  * farope_attn_bwd without the caller workspace: no counterpart in the
  * reference.  For callers that cannot allocate device memory (code under HIP
  * graph capture, serving loops, harnesses that forbid hipMalloc).  The split
- * path's workspace (farope_attn_bwd_workspace_elems: the delta rows, and the
- * partial rows of a lone last key) lives in a static device array of
- * FAROPE_NOALLOC_MAX_ROWS fp32 values that the library holds on every device
- * it runs on until the process ends; calls that need more return
- * FAROPE_ERR_SCRATCH before anything is launched.  Allocates nothing.  Calls on one device share that array, so
+ * path's workspace (the delta rows, and the partial rows of a lone last key)
+ * lives in a static device array of FAROPE_NOALLOC_MAX_ROWS fp32 values that
+ * the library holds on every device it runs on until the process ends; calls
+ * that need more return FAROPE_ERR_SCRATCH before anything is launched.  The
+ * rotated Q rows of farope_attn_bwd_workspace_elems go there too when the
+ * whole workspace fits; otherwise the dK/dV pass rotates Q itself (results
+ * within rounding of farope_attn_bwd's).  Allocates nothing.  Calls on one device share that array, so
  * calls that overlap on one device (concurrent streams or threads) race;
  * calls ordered on one stream do not.  The current device must be the one
  * holding the tensors.
