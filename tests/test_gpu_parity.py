@@ -173,11 +173,13 @@ def test_fp32_compute_is_tight():
 @pytest.mark.parametrize(
     "side,has_cls,D",
     [(7, True, 64), (5, False, 64), (16, True, 64), (14, True, 128), (3, False, 128), (1, True, 64),
-     (14, True, 32), (5, False, 32), (16, True, 32), (14, True, 256), (5, False, 256), (17, True, 256)],
+     (14, True, 32), (5, False, 32), (16, True, 32), (14, True, 256), (5, False, 256), (17, True, 256),
+     (14, False, 64), (14, False, 32)],
 )
 def test_ragged_and_variant_shapes(side, has_cls, D):
     """Ragged N (N % 32 != 0), no-CLS, N > 256 (streamed fwd + split bwd), D=128, D=32,
-    D=256 (the largest power of two the reference's kernels take, FA:146, FA:313), N=2."""
+    D=256 (the largest power of two the reference's kernels take, FA:146, FA:313), N=2,
+    N = 196 / 197 (13 query subtiles of the forward's 256-row item) at D = 32, 64."""
     cfg = dict(B=3, H=5, side=side, has_cls=has_cls, D=D, dtype=torch.bfloat16, scale=1.0, dout="randn")
     q, k, v, do = make_inputs(cfg, DEV, seed=1)
     table = CosSinTable(ROPE_BASE, side, D, device=DEV)
