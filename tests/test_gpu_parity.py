@@ -19,6 +19,8 @@ from tests.cases import (CONFIGS, ROPE_BASE, TOL_MAX, TOL_MEAN, allowed, errors,
 from triton_fused_rope_flash_attn_amd import CosSinTable, TritonAttention, sdpa_triton_fa_rope
 from triton_fused_rope_flash_attn_amd import _lib
 
+from tests import _report
+
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
@@ -26,6 +28,8 @@ DEV = "cuda"
 def _say(msg: str) -> None:
     print(msg, flush=True)
     sys.stdout.flush()
+    if "max_abs_err" in msg or msg.startswith("[fp16 range]"):
+        _report.LINES.append(msg)
 
 
 def _run_ours(q, k, v, do, table, has_cls, autocast_dtype=None, sum_loss=False):
