@@ -13,6 +13,13 @@
  * Tensor conventions: q, k, v, o, dout, dq, dk, dv are [B, H, N, D] with
  * arbitrary element strides (stride[0..3] = b, h, n, d; stride 0 allowed for
  * inputs); lse and delta are contiguous fp32 [B*H, N].
+ *
+ * RoPE table: every entry point that reads the packed table takes its
+ * element count, rope_elems, right after the pointer, and returns
+ * FAROPE_ERR_TABLE unless it equals farope_rope_packed_elems(n_pos,
+ * head_dim / 2) of the call's descriptor.  (The reference never checks the
+ * table against the attention shape, FA:1033, FA:1043-1047, and reads past
+ * a short one.)
  */
 #ifndef FAROPE_H
 #define FAROPE_H
@@ -24,7 +31,7 @@
 extern "C" {
 #endif
 
-#define FAROPE_ABI_VERSION 3
+#define FAROPE_ABI_VERSION 4
 
 typedef enum farope_dtype {
   FAROPE_F32 = 0,
@@ -38,7 +45,8 @@ typedef enum farope_status {
   FAROPE_ERR_HEAD_DIM = 2,    /* head_dim not supported (needs D % 4 == 0; kernels: 32, 64, 128, 256) */
   FAROPE_ERR_SEQ_LEN = 3,     /* seq_len != n_pos + has_cls, or seq_len < 1 */
   FAROPE_ERR_DTYPE = 4,       /* unknown io or compute dtype */
-  FAROPE_ERR_TABLE = 5,       /* RoPE table geometry inconsistent with the call */
+  FAROPE_ERR_TABLE = 5,       /* rope_elems != farope_rope_packed_elems(n_pos, head_dim / 2),
+                                 or farope_rope_pack given n_pos < 1 or an odd / zero d2 */
   FAROPE_ERR_SHAPE = 6,       /* batch/heads not positive or sizes overflow */
   FAROPE_ERR_LAUNCH = 7,      /* the HIP runtime rejected a kernel launch */
   FAROPE_ERR_ALIGN = 8,       /* a pointer is not aligned to its element size */
@@ -96,7 +104,9 @@ int farope_rope_pack(const float* cosp, int64_t cos_stride0, int64_t cos_stride1
 size_t farope_attn_residual_elems(const farope_attn_desc* desc);
 
 /*
- * fp32 elements of farope_attn_bwd's delta_ws: batch * heads * seq_len delta
+ * fp32 elements of farope_attn_bwd's delta_ws.  0 when the one-pass kernel
+ * runs (head_dim 64, seq_len <= 256, 16-bit compute: it keeps delta on chip,
+ * and delta_ws may then be NULL).  Otherwise batch * heads * seq_len delta
  * rows (the reference's D tensor, allocated with M's shape in
  * TritonAttention.backward, FA:1075), plus, when each plane's last key
  * is the only one past the dK/dV kernel's full key blocks at fp16-logit
@@ -120,7 +130,7 @@ int farope_attn_fwd(const farope_attn_desc* desc,
                     const void* q, const int64_t q_stride[4],
                     const void* k, const int64_t k_stride[4],
                     const void* v, const int64_t v_stride[4],
-                    const float* rope_packed,
+                    const float* rope_packed, size_t rope_elems,
                     void* o, const int64_t o_stride[4], void* o_res,
                     float* lse, void* stream);
 
@@ -139,7 +149,7 @@ int farope_attn_bwd_dk_dv(const farope_attn_desc* desc,
                           const void* v, const int64_t v_stride[4],
                           const void* dout, const int64_t dout_stride[4],
                           const float* lse, const float* delta,
-                          const float* rope_packed,
+                          const float* rope_packed, size_t rope_elems,
                           void* dk, const int64_t dk_stride[4],
                           void* dv, const int64_t dv_stride[4], void* stream);
 
@@ -151,7 +161,7 @@ int farope_attn_bwd_dq(const farope_attn_desc* desc,
                        const void* v, const int64_t v_stride[4],
                        const void* dout, const int64_t dout_stride[4],
                        const float* lse, const float* delta,
-                       const float* rope_packed,
+                       const float* rope_packed, size_t rope_elems,
                        void* dq, const int64_t dq_stride[4], void* stream);
 
 /*
@@ -168,7 +178,7 @@ int farope_attn_bwd(const farope_attn_desc* desc,
                     const void* v, const int64_t v_stride[4],
                     const void* o, const int64_t o_stride[4], const void* o_res,
                     const void* dout, const int64_t dout_stride[4],
-                    const float* lse, const float* rope_packed,
+                    const float* lse, const float* rope_packed, size_t rope_elems,
                     void* dq, const int64_t dq_stride[4],
                     void* dk, const int64_t dk_stride[4],
                     void* dv, const int64_t dv_stride[4],
@@ -195,7 +205,7 @@ int farope_attn_bwd_noalloc(const farope_attn_desc* desc,
                             const void* v, const int64_t v_stride[4],
                             const void* o, const int64_t o_stride[4], const void* o_res,
                             const void* dout, const int64_t dout_stride[4],
-                            const float* lse, const float* rope_packed,
+                            const float* lse, const float* rope_packed, size_t rope_elems,
                             void* dq, const int64_t dq_stride[4],
                             void* dk, const int64_t dk_stride[4],
                             void* dv, const int64_t dv_stride[4], void* stream);

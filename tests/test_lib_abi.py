@@ -86,7 +86,9 @@ def test_tile_table(lib, N, D, has_cls, fwd_items, bwd_var):
         (32, 12, 1025, 128, _lib.BF16, _lib.BF16, 4 * 2 * 128, True),   # HiRes: 4 dQ tiles per plane
         (2, 3, 257, 256, _lib.BF16, _lib.BF16, 4 * 2 * 256, True),      # 64-row dQ tiles
         (2, 3, 257, 128, _lib.F16, _lib.BF16, 1 * 2 * 128, True),       # fp16 I/O, bf16 compute
-        (256, 12, 197, 64, _lib.BF16, _lib.BF16, 0, False),             # one-pass backward
+        (256, 12, 197, 64, _lib.BF16, _lib.BF16, None, False),          # one-pass backward: none
+        (1800, 12, 197, 64, _lib.BF16, _lib.BF16, None, False),         # (> 4 Mi rows, still none)
+        (4, 2, 2, 64, _lib.F16, _lib.F16, None, False),                 # N = 2, fp16: one-pass
         (2, 3, 257, 64, _lib.BF16, _lib.BF16, 0, False),                # no fp16 logits at D = 64
         (2, 3, 257, 128, _lib.F16, _lib.F16, 0, False),                 # fp16 compute
         (2, 3, 1100, 128, _lib.BF16, _lib.BF16, 0, True),               # 76 rows past the blocks
@@ -95,11 +97,16 @@ def test_tile_table(lib, N, D, has_cls, fwd_items, bwd_var):
     ],
 )
 def test_bwd_workspace_elems(lib, B, H, N, D, io, ct, extra, hat):
-    """delta rows; one partial dK / dV row pair per dQ tile when the plane's lone
-    last key is summed by those tiles (fp16 logits, N = 1 + k * 256); then, from a
-    64-float boundary, the dQ pass's fp16 Q-hat rows for the dK/dV pass (fp16
-    logits, every row in a dQ tile)."""
+    """No workspace for the one-pass backward (extra None: delta stays on chip).
+    Otherwise delta rows; one partial dK / dV row pair per dQ tile when the
+    plane's lone last key is summed by those tiles (fp16 logits, N = 1 + k * 256);
+    then, from a 64-float boundary, the dQ pass's fp16 Q-hat rows for the dK/dV
+    pass (fp16 logits, every row in a dQ tile)."""
     desc = _lib.make_desc(B, H, N, D, N - 1, True, io, ct, D ** -0.5)
+    if extra is None:
+        assert _lib.tile_config(desc, 1)[0] == 0
+        assert _lib.bwd_workspace_elems(desc) == 0
+        return
     n = B * H * N + B * H * extra
     if hat:
         n = (n + 63) // 64 * 64 + B * H * N * D // 2
@@ -113,11 +120,14 @@ def test_fp32_compute_takes_split_backward(lib):
     assert _lib.tile_config(desc, 1)[0] == 1
 
 
-def _call_fwd(lib, desc, q=16, lse=16, rope=16):
+ROPE_ELEMS = 197 * 64   # farope_rope_packed_elems(196, 32): the table of the descriptors below
+
+
+def _call_fwd(lib, desc, q=16, lse=16, rope=16, rope_elems=ROPE_ELEMS):
     s = _lib.Stride4(0, 0, 0, 1)
     return lib.farope_attn_fwd(
         ctypes.byref(desc) if desc is not None else None,
-        q, s, 16, s, 16, s, rope, 16, s, None, lse, None,
+        q, s, 16, s, 16, s, rope, rope_elems, 16, s, None, lse, None,
     )
 
 
@@ -148,16 +158,54 @@ def test_fwd_rejects_null_and_misaligned(lib):
     assert _call_fwd(lib, desc, rope=24) == _lib.ERR_ALIGN    # table needs 16-byte alignment
 
 
+def test_fwd_rejects_a_table_of_another_geometry(lib):
+    """rope_elems must be farope_rope_packed_elems(n_pos, head_dim / 2)."""
+    desc = _lib.make_desc(2, 3, 197, 64, 196, True, _lib.BF16, _lib.BF16, 0.125)
+    assert lib.farope_rope_packed_elems(196, 32) == ROPE_ELEMS
+    for n in (0, ROPE_ELEMS - 2, ROPE_ELEMS + 64, 197 * 128, 196 * 64):
+        assert _call_fwd(lib, desc, rope_elems=n) == _lib.ERR_TABLE
+    assert _call_fwd(lib, desc, rope=None) == _lib.ERR_NULL
+
+
+def _bwd(lib, desc, o_res=None, lse=16, rope=16, rope_elems=ROPE_ELEMS, dq=16, delta=16):
+    """farope_attn_bwd with placeholder (never dereferenced) device pointers."""
+    s = _lib.Stride4(0, 0, 0, 1)
+    return lib.farope_attn_bwd(ctypes.byref(desc), 16, s, 16, s, 16, s, 16, s, o_res, 16, s, lse,
+                               rope, rope_elems, dq, s, 16, s, 16, s, delta, None)
+
+
+def _bwd_dq(lib, desc, delta=16, rope_elems=ROPE_ELEMS):
+    s = _lib.Stride4(0, 0, 0, 1)
+    return lib.farope_attn_bwd_dq(ctypes.byref(desc), 16, s, 16, s, 16, s, 16, s, 16, delta, 16,
+                                  rope_elems, 16, s, None)
+
+
+def _bwd_dk_dv(lib, desc, dv=16, rope_elems=ROPE_ELEMS):
+    s = _lib.Stride4(0, 0, 0, 1)
+    return lib.farope_attn_bwd_dk_dv(ctypes.byref(desc), 16, s, 16, s, 16, s, 16, s, 16, 16, 16,
+                                     rope_elems, 16, s, dv, s, None)
+
+
+def _bwd_noalloc(lib, desc, rope_elems):
+    s = _lib.Stride4(0, 0, 0, 1)
+    return lib.farope_attn_bwd_noalloc(ctypes.byref(desc), 16, s, 16, s, 16, s, 16, s, None, 16, s,
+                                       16, 16, rope_elems, 16, s, 16, s, 16, s, None)
+
+
 def test_bwd_entry_points_reject_bad_arguments(lib):
     s = _lib.Stride4(0, 0, 0, 1)
     bad = _lib.make_desc(2, 3, 197, 60, 196, True, _lib.BF16, _lib.BF16, 0.125)
-    assert lib.farope_attn_bwd(ctypes.byref(bad), *([16, s] * 4), None, 16, s, 16, 16, *([16, s] * 3), 16, None) == _lib.ERR_HEAD_DIM
+    assert _bwd(lib, bad) == _lib.ERR_HEAD_DIM
     good = _lib.make_desc(2, 3, 197, 64, 196, True, _lib.BF16, _lib.BF16, 0.125)
-    assert lib.farope_attn_bwd(ctypes.byref(good), *([16, s] * 4), None, 16, s, None, 16, *([16, s] * 3), 16, None) == _lib.ERR_NULL
-    assert lib.farope_attn_bwd(ctypes.byref(good), *([16, s] * 4), 24, 16, s, 16, 16, *([16, s] * 3), 16, None) == _lib.ERR_ALIGN
+    assert _bwd(lib, good, lse=None) == _lib.ERR_NULL
+    assert _bwd(lib, good, dq=24 + 1) == _lib.ERR_ALIGN
+    assert _bwd(lib, good, rope=24) == _lib.ERR_ALIGN
+    assert _bwd(lib, good, rope_elems=ROPE_ELEMS + 2) == _lib.ERR_TABLE
     assert lib.farope_attn_bwd_preprocess(ctypes.byref(bad), 16, s, None, 16, s, 16, None) == _lib.ERR_HEAD_DIM
-    assert lib.farope_attn_bwd_dq(ctypes.byref(good), *([16, s] * 4), 16, 3, 16, 16, s, None) == _lib.ERR_ALIGN
-    assert lib.farope_attn_bwd_dk_dv(ctypes.byref(good), *([16, s] * 4), 16, 16, 16, 16, s, None, s, None) == _lib.ERR_NULL
+    assert _bwd_dq(lib, good, delta=3) == _lib.ERR_ALIGN
+    assert _bwd_dq(lib, good, rope_elems=1) == _lib.ERR_TABLE
+    assert _bwd_dk_dv(lib, good, dv=None) == _lib.ERR_NULL
+    assert _bwd_dk_dv(lib, good, rope_elems=196 * 64) == _lib.ERR_TABLE
     assert lib.farope_rope_pack(16, 32, 1, 16, 32, 1, 196, 31, 16, None) == _lib.ERR_TABLE
     assert lib.farope_rope_pack(None, 32, 1, 16, 32, 1, 196, 32, 16, None) == _lib.ERR_NULL
 
@@ -167,11 +215,10 @@ def test_noalloc_bwd_rejects_oversize_before_any_launch(lib):
     workspace (FAROPE_NOALLOC_MAX_ROWS) with FAROPE_ERR_SCRATCH, on the host."""
     m = re.search(r"#define FAROPE_NOALLOC_MAX_ROWS (\d+)", open(HEADER).read())
     assert int(m.group(1)) == _lib.NOALLOC_MAX_ROWS
-    s = _lib.Stride4(0, 0, 0, 1)
     N = 1025   # split path; 4096 planes x 1025 rows > 4 Mi rows
     big = _lib.make_desc(64, 64, N, 128, N - 1, True, _lib.BF16, _lib.BF16, 128 ** -0.5)
     assert 64 * 64 * N > _lib.NOALLOC_MAX_ROWS
-    assert lib.farope_attn_bwd_noalloc(ctypes.byref(big), *([16, s] * 4), None, 16, s, 16, 16, *([16, s] * 3), None) == _lib.ERR_SCRATCH
+    assert _bwd_noalloc(lib, big, lib.farope_rope_packed_elems(N - 1, 64)) == _lib.ERR_SCRATCH
     bad = _lib.make_desc(2, 3, 197, 60, 196, True, _lib.BF16, _lib.BF16, 0.125)
-    assert lib.farope_attn_bwd_noalloc(ctypes.byref(bad), *([16, s] * 4), None, 16, s, 16, 16, *([16, s] * 3), None) == _lib.ERR_HEAD_DIM
+    assert _bwd_noalloc(lib, bad, ROPE_ELEMS) == _lib.ERR_HEAD_DIM
     assert "static workspace" in _lib.strerror(_lib.ERR_SCRATCH)

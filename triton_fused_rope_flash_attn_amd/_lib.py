@@ -62,6 +62,7 @@ _S = ctypes.POINTER(ctypes.c_int64)
 _D = ctypes.POINTER(AttnDesc)
 _I32 = ctypes.c_int32
 _I64 = ctypes.c_int64
+_Z = ctypes.c_size_t
 
 _SIGNATURES = {
     "farope_abi_version": (ctypes.c_int, []),
@@ -70,20 +71,20 @@ _SIGNATURES = {
     "farope_rope_pack": (ctypes.c_int, [_P, _I64, _I64, _P, _I64, _I64, _I32, _I32, _P, _P]),
     "farope_attn_residual_elems": (ctypes.c_size_t, [_D]),
     "farope_attn_bwd_workspace_elems": (ctypes.c_size_t, [_D]),
-    "farope_attn_fwd": (ctypes.c_int, [_D, _P, _S, _P, _S, _P, _S, _P, _P, _S, _P, _P, _P]),
+    "farope_attn_fwd": (ctypes.c_int, [_D, _P, _S, _P, _S, _P, _S, _P, _Z, _P, _S, _P, _P, _P]),
     "farope_attn_bwd_preprocess": (ctypes.c_int, [_D, _P, _S, _P, _P, _S, _P, _P]),
     "farope_attn_bwd_dk_dv": (
         ctypes.c_int,
-        [_D, _P, _S, _P, _S, _P, _S, _P, _S, _P, _P, _P, _P, _S, _P, _S, _P],
+        [_D, _P, _S, _P, _S, _P, _S, _P, _S, _P, _P, _P, _Z, _P, _S, _P, _S, _P],
     ),
-    "farope_attn_bwd_dq": (ctypes.c_int, [_D, _P, _S, _P, _S, _P, _S, _P, _S, _P, _P, _P, _P, _S, _P]),
+    "farope_attn_bwd_dq": (ctypes.c_int, [_D, _P, _S, _P, _S, _P, _S, _P, _S, _P, _P, _P, _Z, _P, _S, _P]),
     "farope_attn_bwd": (
         ctypes.c_int,
-        [_D, _P, _S, _P, _S, _P, _S, _P, _S, _P, _P, _S, _P, _P, _P, _S, _P, _S, _P, _S, _P, _P],
+        [_D, _P, _S, _P, _S, _P, _S, _P, _S, _P, _P, _S, _P, _P, _Z, _P, _S, _P, _S, _P, _S, _P, _P],
     ),
     "farope_attn_bwd_noalloc": (
         ctypes.c_int,
-        [_D, _P, _S, _P, _S, _P, _S, _P, _S, _P, _P, _S, _P, _P, _P, _S, _P, _S, _P, _S, _P],
+        [_D, _P, _S, _P, _S, _P, _S, _P, _S, _P, _P, _S, _P, _P, _Z, _P, _S, _P, _S, _P, _S, _P],
     ),
     "farope_tile_config": (ctypes.c_int, [_D, _I32, ctypes.POINTER(ctypes.c_int32)]),
 }
@@ -170,7 +171,7 @@ def attn_fwd(desc: AttnDesc, q, k, v, rope, o, lse, o_res=None) -> None:
     rc = load().farope_attn_fwd(
         ctypes.byref(desc),
         q.data_ptr(), strides(q), k.data_ptr(), strides(k), v.data_ptr(), strides(v),
-        rope.data_ptr(), o.data_ptr(), strides(o), _ptr(o_res), lse.data_ptr(), stream_of(q),
+        rope.data_ptr(), rope.numel(), o.data_ptr(), strides(o), _ptr(o_res), lse.data_ptr(), stream_of(q),
     )
     check(rc, "farope_attn_fwd")
 
@@ -180,9 +181,9 @@ def attn_bwd(desc: AttnDesc, q, k, v, o, do, lse, rope, dq, dk, dv, delta, o_res
         ctypes.byref(desc),
         q.data_ptr(), strides(q), k.data_ptr(), strides(k), v.data_ptr(), strides(v),
         o.data_ptr(), strides(o), _ptr(o_res), do.data_ptr(), strides(do),
-        lse.data_ptr(), rope.data_ptr(),
+        lse.data_ptr(), rope.data_ptr(), rope.numel(),
         dq.data_ptr(), strides(dq), dk.data_ptr(), strides(dk), dv.data_ptr(), strides(dv),
-        delta.data_ptr(), stream_of(q),
+        _ptr(delta), stream_of(q),
     )
     check(rc, "farope_attn_bwd")
 
@@ -193,7 +194,7 @@ def attn_bwd_noalloc(desc: AttnDesc, q, k, v, o, do, lse, rope, dq, dk, dv, o_re
         ctypes.byref(desc),
         q.data_ptr(), strides(q), k.data_ptr(), strides(k), v.data_ptr(), strides(v),
         o.data_ptr(), strides(o), _ptr(o_res), do.data_ptr(), strides(do),
-        lse.data_ptr(), rope.data_ptr(),
+        lse.data_ptr(), rope.data_ptr(), rope.numel(),
         dq.data_ptr(), strides(dq), dk.data_ptr(), strides(dk), dv.data_ptr(), strides(dv),
         stream_of(q),
     )
@@ -212,7 +213,7 @@ def attn_bwd_dk_dv(desc: AttnDesc, q, k, v, do, lse, delta, rope, dk, dv) -> Non
     rc = load().farope_attn_bwd_dk_dv(
         ctypes.byref(desc),
         q.data_ptr(), strides(q), k.data_ptr(), strides(k), v.data_ptr(), strides(v),
-        do.data_ptr(), strides(do), lse.data_ptr(), delta.data_ptr(), rope.data_ptr(),
+        do.data_ptr(), strides(do), lse.data_ptr(), delta.data_ptr(), rope.data_ptr(), rope.numel(),
         dk.data_ptr(), strides(dk), dv.data_ptr(), strides(dv), stream_of(q),
     )
     check(rc, "farope_attn_bwd_dk_dv")
@@ -222,7 +223,7 @@ def attn_bwd_dq(desc: AttnDesc, q, k, v, do, lse, delta, rope, dq) -> None:
     rc = load().farope_attn_bwd_dq(
         ctypes.byref(desc),
         q.data_ptr(), strides(q), k.data_ptr(), strides(k), v.data_ptr(), strides(v),
-        do.data_ptr(), strides(do), lse.data_ptr(), delta.data_ptr(), rope.data_ptr(),
+        do.data_ptr(), strides(do), lse.data_ptr(), delta.data_ptr(), rope.data_ptr(), rope.numel(),
         dq.data_ptr(), strides(dq), stream_of(q),
     )
     check(rc, "farope_attn_bwd_dq")

@@ -150,8 +150,10 @@ def attn_bwd(
     dv = torch.empty((B, H, N, D), dtype=v.dtype, device=q.device)
     desc = _lib.make_desc(B, H, N, D, n_pos, has_cls, _lib.DTYPE_CODE[q.dtype], compute_dtype,
                           softmax_scale)
-    # delta rows (+ the dQ tiles' partial rows of a lone last key, when used)
-    delta = torch.empty(_lib.bwd_workspace_elems(desc), dtype=torch.float32, device=q.device)
+    # delta rows (+ the dQ tiles' partial rows of a lone last key, when used);
+    # none for the one-pass backward, which keeps delta on chip
+    ws = _lib.bwd_workspace_elems(desc)
+    delta = torch.empty(ws, dtype=torch.float32, device=q.device) if ws else None
     if o_res.numel() and (o_res.shape != q.shape or o_res.dtype != q.dtype or not o_res.is_contiguous()):
         raise ValueError("farope: O_res must be contiguous with Q's shape and dtype, or empty")
     with torch.cuda.device(q.device):

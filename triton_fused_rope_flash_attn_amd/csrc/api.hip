@@ -72,6 +72,15 @@ int check_desc(const farope_attn_desc* d) {
   return FAROPE_OK;
 }
 
+// The packed table a call passes must be the one of its geometry:
+// farope_rope_packed_elems(n_pos, head_dim / 2) fp32 values.
+int check_table(const farope_attn_desc* d, const float* rope, size_t elems) {
+  if (!rope) return FAROPE_ERR_NULL;
+  if (reinterpret_cast<uintptr_t>(rope) % 16) return FAROPE_ERR_ALIGN;
+  if (elems != (size_t)(d->n_pos + 1) * (size_t)d->head_dim) return FAROPE_ERR_TABLE;
+  return FAROPE_OK;
+}
+
 int check_ptr(const void* p, int es) {
   if (!p) return FAROPE_ERR_NULL;
   if (reinterpret_cast<uintptr_t>(p) % es) return FAROPE_ERR_ALIGN;
@@ -221,8 +230,8 @@ struct BwdWs {
 };
 BwdWs bwd_ws(const farope_attn_desc* d, bool with_hat) {
   const int64_t planes = (int64_t)d->batch * d->heads, rows = planes * d->seq_len;
+  if (bwd_fused(d)) return BwdWs{0, 0, 0};   // the one-pass kernel keeps delta on chip
   BwdWs w{rows, 0, rows};
-  if (bwd_fused(d)) return w;
   if (key_from_dq(d, true)) {
     const int nb = main_blocks((int)planes, d->seq_len, bwd_dq_block_rows(d->head_dim, d->compute_dtype));
     w.total += planes * nb * 2 * d->head_dim;
@@ -238,7 +247,7 @@ int64_t bwd_ws_elems(const farope_attn_desc* d) { return bwd_ws(d, false).total;
 int bwd_impl(const farope_attn_desc* desc, const void* q, const int64_t q_stride[4],
              const void* k, const int64_t k_stride[4], const void* v, const int64_t v_stride[4],
              const void* o, const int64_t o_stride[4], const void* o_res, const void* dout,
-             const int64_t dout_stride[4], const float* lse, const float* rope_packed, void* dq,
+             const int64_t dout_stride[4], const float* lse, const float* rope_packed, size_t rope_elems, void* dq,
              const int64_t dq_stride[4], void* dk, const int64_t dk_stride[4], void* dv,
              const int64_t dv_stride[4], float* delta_ws, bool static_ws, void* stream) {
   FAROPE_TRY(check_desc(desc));
@@ -255,14 +264,16 @@ int bwd_impl(const farope_attn_desc* desc, const void* q, const int64_t q_stride
   FAROPE_TRY(check_ptr(dk, es));
   FAROPE_TRY(check_ptr(dv, es));
   FAROPE_TRY(check_ptr(lse, 4));
-  FAROPE_TRY(check_ptr(rope_packed, 16));
+  FAROPE_TRY(check_table(desc, rope_packed, rope_elems));
   const bool fused = bwd_fused(desc);
-  if (static_ws) {
-    // the split path's delta rows go to this device's static scratch array
-    if (bwd_ws_elems(desc) > kScratchFloats) return FAROPE_ERR_SCRATCH;
-    FAROPE_TRY(scratch_ptr(&delta_ws));
-  } else if (!fused) {
-    FAROPE_TRY(check_ptr(delta_ws, 4));
+  if (!fused) {
+    if (static_ws) {
+      // the split path's delta rows go to this device's static scratch array
+      if (bwd_ws_elems(desc) > kScratchFloats) return FAROPE_ERR_SCRATCH;
+      FAROPE_TRY(scratch_ptr(&delta_ws));
+    } else {
+      FAROPE_TRY(check_ptr(delta_ws, 4));
+    }
   }
   if (o_res) FAROPE_TRY(check_ptr(o_res, 16));
   BwdParams p = {};
@@ -321,7 +332,8 @@ const char* farope_strerror(int status) {
       return "farope: unsupported head_dim (must be divisible by 4; kernels exist for 32, 64, 128 and 256)";
     case FAROPE_ERR_SEQ_LEN: return "farope: seq_len must equal n_pos + has_cls";
     case FAROPE_ERR_DTYPE: return "farope: unsupported dtype (float32, float16, bfloat16)";
-    case FAROPE_ERR_TABLE: return "farope: RoPE table geometry does not match the call";
+    case FAROPE_ERR_TABLE:
+      return "farope: RoPE table geometry does not match the call (rope_elems must be farope_rope_packed_elems(n_pos, head_dim / 2))";
     case FAROPE_ERR_SHAPE: return "farope: batch/heads must be positive and B*H <= 2^30";
     case FAROPE_ERR_LAUNCH: return "farope: HIP kernel launch failed";
     case FAROPE_ERR_ALIGN: return "farope: pointer not aligned to its element size";
@@ -381,7 +393,7 @@ size_t farope_attn_residual_elems(const farope_attn_desc* desc) {
 
 int farope_attn_fwd(const farope_attn_desc* desc, const void* q, const int64_t q_stride[4],
                     const void* k, const int64_t k_stride[4], const void* v,
-                    const int64_t v_stride[4], const float* rope_packed, void* o,
+                    const int64_t v_stride[4], const float* rope_packed, size_t rope_elems, void* o,
                     const int64_t o_stride[4], void* o_res, float* lse, void* stream) {
   FAROPE_TRY(check_desc(desc));
   if (!q_stride || !k_stride || !v_stride || !o_stride) return FAROPE_ERR_NULL;
@@ -391,7 +403,7 @@ int farope_attn_fwd(const farope_attn_desc* desc, const void* q, const int64_t q
   FAROPE_TRY(check_ptr(v, es));
   FAROPE_TRY(check_ptr(o, es));
   FAROPE_TRY(check_ptr(lse, 4));
-  FAROPE_TRY(check_ptr(rope_packed, 16));
+  FAROPE_TRY(check_table(desc, rope_packed, rope_elems));
   if (o_res) FAROPE_TRY(check_ptr(o_res, 16));
 
   FwdParams p;
@@ -443,7 +455,7 @@ int farope_attn_bwd_dk_dv(const farope_attn_desc* desc, const void* q, const int
                           const void* k, const int64_t k_stride[4], const void* v,
                           const int64_t v_stride[4], const void* dout,
                           const int64_t dout_stride[4], const float* lse, const float* delta,
-                          const float* rope_packed, void* dk, const int64_t dk_stride[4],
+                          const float* rope_packed, size_t rope_elems, void* dk, const int64_t dk_stride[4],
                           void* dv, const int64_t dv_stride[4], void* stream) {
   FAROPE_TRY(check_desc(desc));
   if (!q_stride || !k_stride || !v_stride || !dout_stride || !dk_stride || !dv_stride)
@@ -457,7 +469,7 @@ int farope_attn_bwd_dk_dv(const farope_attn_desc* desc, const void* q, const int
   FAROPE_TRY(check_ptr(dv, es));
   FAROPE_TRY(check_ptr(lse, 4));
   FAROPE_TRY(check_ptr(delta, 4));
-  FAROPE_TRY(check_ptr(rope_packed, 16));
+  FAROPE_TRY(check_table(desc, rope_packed, rope_elems));
   BwdParams p = {};
   fill_common(p, desc, rope_packed);
   p.q = q; p.k = k; p.v = v; p.dout = dout; p.dk = dk; p.dv = dv;
@@ -476,7 +488,7 @@ int farope_attn_bwd_dk_dv(const farope_attn_desc* desc, const void* q, const int
 int farope_attn_bwd_dq(const farope_attn_desc* desc, const void* q, const int64_t q_stride[4],
                        const void* k, const int64_t k_stride[4], const void* v,
                        const int64_t v_stride[4], const void* dout, const int64_t dout_stride[4],
-                       const float* lse, const float* delta, const float* rope_packed, void* dq,
+                       const float* lse, const float* delta, const float* rope_packed, size_t rope_elems, void* dq,
                        const int64_t dq_stride[4], void* stream) {
   FAROPE_TRY(check_desc(desc));
   if (!q_stride || !k_stride || !v_stride || !dout_stride || !dq_stride) return FAROPE_ERR_NULL;
@@ -488,7 +500,7 @@ int farope_attn_bwd_dq(const farope_attn_desc* desc, const void* q, const int64_
   FAROPE_TRY(check_ptr(dq, es));
   FAROPE_TRY(check_ptr(lse, 4));
   FAROPE_TRY(check_ptr(delta, 4));
-  FAROPE_TRY(check_ptr(rope_packed, 16));
+  FAROPE_TRY(check_table(desc, rope_packed, rope_elems));
   BwdParams p = {};
   fill_common(p, desc, rope_packed);
   p.q = q; p.k = k; p.v = v; p.dout = dout; p.dq = dq;
@@ -507,11 +519,11 @@ int farope_attn_bwd(const farope_attn_desc* desc, const void* q, const int64_t q
                     const void* k, const int64_t k_stride[4], const void* v,
                     const int64_t v_stride[4], const void* o, const int64_t o_stride[4],
                     const void* o_res, const void* dout, const int64_t dout_stride[4], const float* lse,
-                    const float* rope_packed, void* dq, const int64_t dq_stride[4], void* dk,
+                    const float* rope_packed, size_t rope_elems, void* dq, const int64_t dq_stride[4], void* dk,
                     const int64_t dk_stride[4], void* dv, const int64_t dv_stride[4],
                     float* delta_ws, void* stream) {
   return bwd_impl(desc, q, q_stride, k, k_stride, v, v_stride, o, o_stride, o_res, dout, dout_stride,
-                  lse, rope_packed, dq, dq_stride, dk, dk_stride, dv, dv_stride, delta_ws, false, stream);
+                  lse, rope_packed, rope_elems, dq, dq_stride, dk, dk_stride, dv, dv_stride, delta_ws, false, stream);
 }
 
 int farope_attn_bwd_noalloc(const farope_attn_desc* desc, const void* q,
@@ -519,11 +531,11 @@ int farope_attn_bwd_noalloc(const farope_attn_desc* desc, const void* q,
                             const void* v, const int64_t v_stride[4], const void* o,
                             const int64_t o_stride[4], const void* o_res, const void* dout,
                             const int64_t dout_stride[4], const float* lse,
-                            const float* rope_packed, void* dq, const int64_t dq_stride[4],
+                            const float* rope_packed, size_t rope_elems, void* dq, const int64_t dq_stride[4],
                             void* dk, const int64_t dk_stride[4], void* dv,
                             const int64_t dv_stride[4], void* stream) {
   return bwd_impl(desc, q, q_stride, k, k_stride, v, v_stride, o, o_stride, o_res, dout, dout_stride,
-                  lse, rope_packed, dq, dq_stride, dk, dk_stride, dv, dv_stride, nullptr, true, stream);
+                  lse, rope_packed, rope_elems, dq, dq_stride, dk, dk_stride, dv, dv_stride, nullptr, true, stream);
 }
 
 }  // extern "C"

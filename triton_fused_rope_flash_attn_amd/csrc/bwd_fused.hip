@@ -72,10 +72,15 @@ __device__ __forceinline__ f32x4 tab_chunk(const float* t, int row, int c) {
 
 // VEC: every tensor of the call allows 16-byte vector access (decided on the
 // host); the generic instantiation gathers element by element instead.
-// NKB: 32-key blocks summed by the dQ products, 8 or (for N = 193 .. 224, the
-// ViT-S/B planes) 7; dS^T rows and K-hat rows of keys >= N are zero, so
-// blocks beyond the plane's keys add nothing.
-template <typename IO, int CT, bool VEC, int NKB>
+// NKB: 32-key blocks summed by the dQ products, 8, 7 (for N = 193 .. 224, the
+// ViT-S/B planes) or 1 (N <= 32); dS^T rows and K-hat rows of keys >= N are
+// zero, so blocks beyond the plane's keys add nothing.
+// XD (N <= 32, every key of the plane in wave 0): delta = sum_k P dP, formed
+// from the sweep's own fp32 P and dP by a 16-lane sum, instead of
+// rowsum(dO * O) from the bf16-stored O.  Both are delta = dO . O exactly;
+// with a handful of keys dP - delta is a small difference of near-equal
+// terms, and the rounding of the stored O then dominates dS.
+template <typename IO, int CT, bool VEC, int NKB, bool XD>
 __global__ void __launch_bounds__(kPlaneNW * 64)
 bwd_plane_kernel(const BwdParams p) {
   using C = Comp<CT>;
@@ -413,7 +418,7 @@ bwd_plane_kernel(const BwdParams p) {
 #pragma unroll
         for (int u = 0; u < NUA; ++u) {
           sacc[u] = nl2;
-          pacc[u] = ndl;
+          pacc[u] = XD ? f32x4{0.f, 0.f, 0.f, 0.f} : ndl;
         }
         const int qr = 16 * h + lr;
 #pragma unroll
@@ -426,13 +431,27 @@ bwd_plane_kernel(const BwdParams p) {
             pacc[u] = C::mma(b, vf[u][s], pacc[u]);
           }
         }
+        // XD: delta of queries q0 + i = sum over the wave's 32 keys (lanes lr,
+        // subtiles u) of P dP; keys >= N have dP = 0, queries >= N P = 0
+        float xdl[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (XD) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float t = 0.f;
+#pragma unroll
+            for (int u = 0; u < NUA; ++u)
+              t = __builtin_fmaf(__builtin_amdgcn_fmed3f(fast_exp2(sacc[u][i]), 0.f, 1.f), pacc[u][i], t);
+            t = dpp_sum8(t);
+            xdl[i] = t + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t), 0x140, 0xF, 0xF, false));   // row_mirror
+          }
+        }
 #pragma unroll
         for (int u = 0; u < NUA; ++u) {
           float pv[4], dsv[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) pv[i] = __builtin_amdgcn_fmed3f(fast_exp2(sacc[u][i]), 0.f, 1.f);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) dsv[i] = pv[i] * pacc[u][i];
+          for (int i = 0; i < 4; ++i) dsv[i] = pv[i] * (XD ? pacc[u][i] - xdl[i] : pacc[u][i]);
           C::set2(pf[u], 2 * h, pv[0], pv[1]);
           C::set2(pf[u], 2 * h + 1, pv[2], pv[3]);
           C::set2(dsf[u], 2 * h, dsv[0], dsv[1]);
@@ -643,9 +662,10 @@ static hipError_t fused_launch(const BwdParams& p0, hipStream_t st) {
   BwdParams p = p0;
   const bool vec = p.vec_q && p.vec_k && p.vec_v && p.vec_o && p.vec_do && p.vec_dq && p.vec_dk &&
                    p.vec_dv;
-  const bool nkb7 = (p.N + 31) / 32 == 7;
-  auto kern = vec ? (nkb7 ? bwd_plane_kernel<IO, CT, true, 7> : bwd_plane_kernel<IO, CT, true, 8>)
-                  : bwd_plane_kernel<IO, CT, false, 8>;
+  const bool nkb7 = (p.N + 31) / 32 == 7, small = p.N <= 32;
+  auto kern = small ? (vec ? bwd_plane_kernel<IO, CT, true, 1, true> : bwd_plane_kernel<IO, CT, false, 1, true>)
+              : vec ? (nkb7 ? bwd_plane_kernel<IO, CT, true, 7, false> : bwd_plane_kernel<IO, CT, true, 8, false>)
+                    : bwd_plane_kernel<IO, CT, false, 8, false>;
   const size_t tab_bytes = (size_t)p.N * 64 * sizeof(float);   // LDS copy of the RoPE rows
   const int grid = persistent_grid(reinterpret_cast<const void*>(kern), kPlaneNW * 64, p.B * p.H,
                                    tab_bytes);
