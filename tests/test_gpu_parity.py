@@ -67,6 +67,23 @@ def _torch_bf16(q, k, v, do, table, has_cls):
     return o.detach(), qq.grad, kk.grad, vv.grad
 
 
+def _paths_agree(tag, got, want, ref, mult_max=3.0, mult_mean=2.0):
+    """Two backward paths on the same inputs: each gradient of `got` differs
+    from `want` by at most `mult_max` / `mult_mean` x the bf16 storage floor of
+    the fp32 oracle `ref` (max / mean), the scale at which two correct bf16
+    results differ (each is itself held to about 2x that floor against the
+    oracle, so their difference can reach the sum of both errors)."""
+    fails = []
+    for name, a, b, r in zip(("dQ", "dK", "dV"), got, want, ref):
+        mx, mn = errors(a, b)
+        fmx, fmn = rounding_floor(r, torch.bfloat16)
+        _say(f"[{tag}] {name}: max_abs_err={mx:.3e} mean_abs_err={mn:.3e} between the paths "
+             f"(bound {mult_max * fmx:.2e}/{mult_mean * fmn:.2e}, {mult_max:g}x / {mult_mean:g}x the storage floor)")
+        if mx > mult_max * fmx or mn > mult_mean * fmn:
+            fails.append(f"{name}: max {mx:.3e} mean {mn:.3e}")
+    assert not fails, f"{tag}: " + "; ".join(fails)
+
+
 def _compare(tag, ours, ref, tol_max=TOL_MAX, tol_mean=TOL_MEAN, out_dtype=None, other=None):
     """Check max/mean abs error of ours vs ref.
 
@@ -224,7 +241,10 @@ def test_tail_rows(side, has_cls, D, B, H, io):
 
 def test_tail_rows_generic_strides_and_split_entry_points():
     """Tail rows through the generic (d-strided) loads, and through the reference-style
-    preprocess + dk_dv + dq entry points, which must give the one-call backward's bits."""
+    preprocess + dk_dv + dq entry points.  Those run other kernels than the one-call
+    backward (the dK/dV kernel with split-bf16 dS, the fp32 tail-key kernel, rotating Q
+    themselves), so they agree with it within a small multiple of the bf16 storage floor,
+    not bit for bit."""
     B, H, side, D = 2, 2, 16, 128
     N = side * side + 1
     g = torch.Generator().manual_seed(6)
@@ -249,10 +269,8 @@ def test_tail_rows_generic_strides_and_split_entry_points():
     _lib.attn_bwd_dk_dv(desc, q, k, v, do, lse, delta, rope, dk2, dv2)
     _lib.attn_bwd_dq(desc, q, k, v, do, lse, delta, rope, dq2)
     torch.cuda.synchronize()
-    for name, a, b in (("dQ", dq2, dq), ("dK", dk2, dk), ("dV", dv2, dv)):
-        mx, _ = errors(a, b)
-        _say(f"[tail split-vs-one-call] {name}: max diff {mx:.3e}")
-        assert mx < 1e-2
+    _compare("tail entry points", (o, dq2, dk2, dv2), ref, out_dtype=torch.bfloat16)
+    _paths_agree("tail entry points vs one-call", (dq2, dk2, dv2), (dq, dk, dv), ref[1:])
 
 
 def test_strided_qkv_views():
@@ -345,7 +363,9 @@ def test_triton_attention_apply_signature():
 
 
 def test_split_entry_points_match_fused():
-    """preprocess + dk_dv + dq entry points (reference launch structure) == one-call backward."""
+    """preprocess + dk_dv + dq entry points (reference launch structure) against the
+    one-call backward (here the one-pass plane kernel): both within the north-star
+    bound of the oracle, and within a small multiple of the bf16 storage floor of each other."""
     cfg = dict(CONFIGS["vit_b"], B=4)
     q, k, v, do = make_inputs(cfg, DEV)
     table = CosSinTable(ROPE_BASE, 14, 64, device=DEV)
@@ -363,10 +383,9 @@ def test_split_entry_points_match_fused():
     torch.cuda.synchronize()
     ref_delta = (do.float() * o.float()).sum(-1)
     assert errors(delta, ref_delta)[0] < 1e-3
-    for name, a, b in (("dQ", dq2, dq), ("dK", dk2, dk), ("dV", dv2, dv)):
-        mx, _ = errors(a, b)
-        _say(f"[split-vs-fused] {name}: max diff {mx:.3e}")
-        assert mx < 1e-2
+    ref = _ref(q, k, v, do, table, True)
+    _compare("entry points", (o, dq2, dk2, dv2), ref, out_dtype=torch.bfloat16)
+    _paths_agree("entry points vs one-pass", (dq2, dk2, dv2), (dq, dk, dv), ref[1:])
 
 
 def test_deterministic():

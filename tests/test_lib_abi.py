@@ -65,8 +65,8 @@ def test_rope_packed_elems(lib):
 
 @pytest.mark.parametrize(
     "N,D,has_cls,fwd_items,bwd_var",
-    [(197, 64, 1, 1, 0), (256, 64, 0, 1, 0), (257, 64, 1, 1, 1), (1025, 128, 1, 4, 1), (197, 128, 1, 1, 1),
-     (197, 256, 1, 3, 1), (257, 256, 1, 4, 1), (1100, 128, 1, 5, 1)],
+    [(197, 64, 1, 1, 0), (256, 64, 0, 1, 0), (257, 64, 1, 1, 1), (1025, 128, 1, 4, 2), (197, 128, 1, 1, 2),
+     (197, 256, 1, 3, 1), (257, 256, 1, 4, 1), (1100, 128, 1, 5, 2)],
 )
 def test_tile_table(lib, N, D, has_cls, fwd_items, bwd_var):
     desc = _lib.make_desc(8, 12, N, D, N - has_cls, has_cls, _lib.BF16, _lib.BF16, D ** -0.5)
@@ -101,7 +101,9 @@ def test_bwd_workspace_elems(lib, B, H, N, D, io, ct, extra, hat):
     Otherwise delta rows; one partial dK / dV row pair per dQ tile when the
     plane's lone last key is summed by those tiles (fp16 logits, N = 1 + k * 256);
     then, from a 64-float boundary, the dQ pass's fp16 Q-hat rows for the dK/dV
-    pass (fp16 logits, every row in a dQ tile)."""
+    pass (fp16 logits, every row in a dQ tile); then, for the key-tile kernel
+    with fp16 dS products (those shapes at head_dim 128), from a 64-float
+    boundary, a {|dO|, max |Q-hat|} pair per row."""
     desc = _lib.make_desc(B, H, N, D, N - 1, True, io, ct, D ** -0.5)
     if extra is None:
         assert _lib.tile_config(desc, 1)[0] == 0
@@ -110,6 +112,9 @@ def test_bwd_workspace_elems(lib, B, H, N, D, io, ct, extra, hat):
     n = B * H * N + B * H * extra
     if hat:
         n = (n + 63) // 64 * 64 + B * H * N * D // 2
+    if hat and D == 128:
+        assert _lib.tile_config(desc, 1)[0] == 2
+        n = (n + 63) // 64 * 64 + 2 * B * H * N
     assert _lib.bwd_workspace_elems(desc) == n
     bad = _lib.make_desc(B, H, N, 60, N - 1, True, io, ct, 0.125)
     assert _lib.bwd_workspace_elems(bad) == 0

@@ -20,7 +20,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 INCLUDE = os.path.join(REPO_DIR, "include")
 LIB_NAME = "libfarope.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["api.hip", "fwd.hip", "bwd.hip", "bwd_fused.hip", "tail.hip"]
+SOURCES = ["api.hip", "fwd.hip", "bwd.hip", "bwd_fused.hip", "bwd_keys.hip", "tail.hip"]
 ARCH = "gfx950"
 
 

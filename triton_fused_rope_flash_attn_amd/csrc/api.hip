@@ -190,7 +190,10 @@ int dkdv_pass(BwdParams p, const farope_attn_desc* d, hipStream_t st) {
   const int D = d->head_dim, rows = bwd_dkdv_block_rows(D, d->compute_dtype);
   const int tail = tail_of(p.B * p.H, p.N, rows);
   p.n_blk = main_blocks(p.B * p.H, p.N, rows);
-  FAROPE_TRY(launch_rc(launch_bwd_dkdv(p, d->io_dtype, d->compute_dtype, D, st)));
+  if (p.row_stat)   // the dQ pass wrote the statistics the key tiles need
+    FAROPE_TRY(launch_rc(launch_bwd_keys(p, d->io_dtype, st)));
+  else
+    FAROPE_TRY(launch_rc(launch_bwd_dkdv(p, d->io_dtype, d->compute_dtype, D, st)));
   if (tail && p.xk_ws) {
     const int nparts = main_blocks(p.B * p.H, p.N, bwd_dq_block_rows(D, d->compute_dtype));
     FAROPE_TRY(launch_rc(launch_bwd_tail_key_merge(p, d->io_dtype, D, nparts, st)));
@@ -243,6 +246,20 @@ BwdWs bwd_ws(const farope_attn_desc* d, bool with_hat) {
   return w;
 }
 int64_t bwd_ws_elems(const farope_attn_desc* d) { return bwd_ws(d, false).total; }
+
+// Key tiles with fp16 dS products (bwd_keys.hip) in place of the dK/dV
+// kernel: 16-bit I/O, bf16 compute, head_dim 128, with the dQ pass's rotated
+// Q rows (the call also needs vector access to every tensor, checked there).
+bool keys_possible(const farope_attn_desc* d) {
+  return qhat_possible(d) && d->head_dim == kKeysRows && d->compute_dtype == FAROPE_BF16;
+}
+// Caller workspace of farope_attn_bwd: bwd_ws, then (keys_possible, from a
+// 256-byte boundary) one {|dO|_2, max |Q-hat c2|} pair per query row.
+int64_t stat_offset(const farope_attn_desc* d) { return (bwd_ws(d, true).total + 63) & ~int64_t(63); }
+int64_t bwd_caller_ws(const farope_attn_desc* d) {
+  if (!keys_possible(d)) return bwd_ws(d, true).total;
+  return stat_offset(d) + 2 * (int64_t)d->batch * d->heads * d->seq_len;
+}
 
 int bwd_impl(const farope_attn_desc* desc, const void* q, const int64_t q_stride[4],
              const void* k, const int64_t k_stride[4], const void* v, const int64_t v_stride[4],
@@ -314,6 +331,11 @@ int bwd_impl(const farope_attn_desc* desc, const void* q, const int64_t q_stride
         reinterpret_cast<uintptr_t>(hat) % 16 == 0)
       p.qhat_f = hat;
   }
+  // the key tiles with fp16 dS products take the dK/dV pass (the static
+  // workspace only when all of it fits)
+  if (p.qhat_f && keys_possible(desc) && p.vec_k && p.vec_v && p.vec_o && p.vec_dq && p.vec_dk &&
+      p.vec_dv && (!static_ws || bwd_caller_ws(desc) <= kScratchFloats))
+    p.row_stat = delta_ws + stat_offset(desc);
   FAROPE_TRY(dq_pass(p, desc, true, st));
   return dkdv_pass(p, desc, st);
 }
@@ -372,7 +394,7 @@ int farope_tile_config(const farope_attn_desc* desc, int32_t which, int32_t out[
     out[3] = fwd_threads(D);
   } else {
     const bool fu = bwd_fused(desc);
-    out[0] = fu ? BWD_FUSED : BWD_SPLIT;
+    out[0] = fu ? BWD_FUSED : keys_possible(desc) ? BWD_SPLIT16 : BWD_SPLIT;
     out[1] = fu ? bwd_fused_rows() : bwd_dkdv_block_rows(D, desc->compute_dtype);
     out[2] = fu ? cdiv(N, out[1]) : main_blocks(desc->batch * desc->heads, N, out[1]);
     out[3] = fu ? 512 : bwd_dkdv_threads(D, desc->compute_dtype);
@@ -382,7 +404,7 @@ int farope_tile_config(const farope_attn_desc* desc, int32_t which, int32_t out[
 
 size_t farope_attn_bwd_workspace_elems(const farope_attn_desc* desc) {
   if (check_desc(desc) != FAROPE_OK) return 0;
-  return (size_t)bwd_ws(desc, true).total;
+  return (size_t)bwd_caller_ws(desc);
 }
 
 size_t farope_attn_residual_elems(const farope_attn_desc* desc) {

@@ -76,10 +76,15 @@ __global__ void __launch_bounds__(256) bwd_pre_kernel(const BwdParams p) {
 // the plane, rows >= N read 0); their table rows are read when the block is
 // committed.  Otherwise each block is loaded synchronously.
 // FS (bf16 compute, head_dim >= 128): logits from fp16 operands as in the
-// forward pass (an fp16 K-hat tile next to the bf16 one the dQ product
-// reads; Q-hat in registers), and dQ-hat from dS = hi + lo:
-// dQ-hat^T += K-hat^T dS_hi^T + K-hat^T dS_lo^T.  A tile whose Q-hat or
-// K-hat reaches 2^12 is computed again with scaled logit operands.
+// forward pass (the fp16 K-hat * fk tile in LDS, Q-hat in registers), and
+// dQ-hat^T += (K-hat fk)^T (sig dS)^T with both operands in fp16 (one MFMA,
+// 11 significant bits each).  A tile whose Q-hat or K-hat reaches 2^12 is
+// computed again with scaled logit operands, and one whose largest |sig dS|
+// left [2^-10, 2^15) (fp16 overflow, or values deep in its subnormal range)
+// is computed again with sig = the power of two that puts it in
+// [2^14, 2^15) (sig = 1 first).  Nothing is stored before a pass is kept.
+// With p.row_stat the tile also writes each row's {|dO|_2, max |Q-hat c2|}
+// for the key-tile kernel (bwd_keys.hip).
 template <typename IO, int CT, int D, int NW, int QT, int KVS, bool WRITE_DELTA, bool VEC, bool FS>
 __global__ void __launch_bounds__(NW * 64)
 bwd_dq_kernel(const BwdParams p) {
@@ -99,11 +104,11 @@ bwd_dq_kernel(const BwdParams p) {
   constexpr bool TR = sizeof(S) == 2;
 
   static_assert(!FS || CT == DT_BF16, "fp16 logit operands go with bf16 compute");
-  __shared__ __attribute__((aligned(16))) S sK[KVS * LDK];
-  __shared__ __attribute__((aligned(16))) f16 sKf[FS ? KVS * LDK : 8];   // FS: fp16 K-hat
+  __shared__ __attribute__((aligned(16))) S sK[FS ? 8 : KVS * LDK];    // K-hat (non-FS)
+  __shared__ __attribute__((aligned(16))) f16 sKf[FS ? KVS * LDK : 8];   // FS: fp16 K-hat * fk
   __shared__ __attribute__((aligned(16))) S sKt[TR ? 8 : D * LDT];
   __shared__ __attribute__((aligned(16))) S sV[KVS * LDK];
-  __shared__ u32x2 sRange[FS ? NW : 1];   // FS: per-wave max |Q-hat|, |K-hat| bits
+  __shared__ u32x4 sRange[FS ? NW : 1];   // FS: per-wave max |Q-hat|, |K-hat|, |sig dS| bits
   // XR: the plane's last row, when it is the only one past the full query
   // blocks (p.x_rows == 1), rides along one tile of the plane instead of a
   // tail kernel that would read the plane's K and V again.  Its logits, dP
@@ -140,10 +145,11 @@ bwd_dq_kernel(const BwdParams p) {
   // FS: largest |Q-hat| (scaled) and |K-hat| this thread converted in the
   // current pass; the operand scales and the logit factor 1 / (fq fk) of a
   // rescaled pass (all 1 otherwise)
-  float amax_q = 0.f, amax_k = 0.f;
-  float fq = 1.f, fk = 1.f, fsc = 1.f;
+  float amax_q = 0.f, amax_k = 0.f, amax_s = 0.f;
+  float fq = 1.f, fk = 1.f, fsc = 1.f, sig = 1.f;
   bool rescaled = false;
-  for (;;) {   // one pass, or two when FS rescales
+  int npass = 0;
+  for (;;) {   // one pass, or up to three when FS rescales
   // (FS: the lane index is opaque to the compiler, so that no lane-dependent
   // address of the pass is hoisted out of this loop to hold registers)
   const int tid = FS ? opaque(thread_id()) : thread_id();
@@ -158,7 +164,7 @@ bwd_dq_kernel(const BwdParams p) {
   for (int t = 0; t < QT; ++t) {
     const int row = qblk * QROWS + (wave * QT + t) * 16 + lr;
     qrow[t] = row;
-    float dsum = 0.f;
+    float dsum = 0.f, gn2 = 0.f, qmr = 0.f;   // (FS: the row statistics)
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const int c0 = 32 * s + 8 * lg;
@@ -191,10 +197,19 @@ bwd_dq_kernel(const BwdParams p) {
         for (int e = 0; e < 8; ++e) x[e] *= qs;
         amax_q = amax8(amax_q, x);
         qf[t][s].v = to_f16x8(x);
+        qmr = amax8(qmr, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) gn2 = __builtin_fmaf(g[e], g[e], gn2);
       } else {
         qf[t][s] = C::make(x);
       }
       gf[t][s] = C::make(g);
+    }
+    if constexpr (FS) {
+      if (p.row_stat != nullptr && npass == 0) {   // (uniform; first pass: fq = 1)
+        const float gn = __builtin_sqrtf(group4_sum(gn2)), qm = group4_max(qmr);
+        if (lg == 0 && row < N) reinterpret_cast<float2*>(p.row_stat)[prow + row] = make_float2(gn, qm);
+      }
     }
     if (WRITE_DELTA) {
       dsum = group4_sum(dsum);
@@ -221,6 +236,23 @@ bwd_dq_kernel(const BwdParams p) {
         *reinterpret_cast<f16x8*>(static_cast<f16*>(p.qhat_f) + (prow + row) * D + c0) = to_f16x8(x);
       load8(G + row * p.sdo[2] + c0 * p.sdo[3], p.sdo[3], p.vec_do, g);
       C::put8(&sXg[c0], g);
+      if (p.row_stat != nullptr && npass == 0) {
+        // over the D/8 active lanes, as delta below
+        float gn2 = 0.f, qm = amax8(0.f, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) gn2 = __builtin_fmaf(g[e], g[e], gn2);
+        gn2 = dpp_sum8(gn2);
+        gn2 += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(gn2), 0x128, 0xF, 0xF, false));
+        qm = fmaxf(qm, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(qm), 0xB1, 0xF, 0xF, false)));
+        qm = fmaxf(qm, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(qm), 0x4E, 0xF, 0xF, false)));
+        qm = fmaxf(qm, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(qm), 0x141, 0xF, 0xF, false)));
+        qm = fmaxf(qm, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(qm), 0x128, 0xF, 0xF, false)));
+        if constexpr (D / 8 >= 32) {
+          gn2 = xor16_pair_op_sum(gn2);
+          qm = xor16_pair_op_max(qm);
+        }
+        if (lane == 0) reinterpret_cast<float2*>(p.row_stat)[prow + row] = make_float2(__builtin_sqrtf(gn2), qm);
+      }
       float dsum;
       if (WRITE_DELTA) {
         float o[8];
@@ -249,8 +281,9 @@ bwd_dq_kernel(const BwdParams p) {
   }
   if constexpr (FS) amax_q = opaque(amax_q);
   const bool wave_active = qblk * QROWS + wave * QT * 16 < N;
-  // K-hat is staged pre-scaled by scale * log2(e) (fp16 operands: unscaled)
-  const float dq_scale = FS ? p.scale : p.scale / p.scale_log2;
+  // K-hat is staged pre-scaled by scale * log2(e); with fp16 operands it is
+  // staged times fk and the dQ product takes sig dS
+  const float dq_scale = FS ? p.scale / (fk * sig) : p.scale / p.scale_log2;
 
   f32x4 dqacc[QT][DT];
 #pragma unroll
@@ -261,15 +294,14 @@ bwd_dq_kernel(const BwdParams p) {
   // K-hat row segment -> sK, pre-scaled by softmax_scale * log2(e) as in the
   // forward pass, so that both passes see bit-identical logits in log2 units
   // (dQ's scale divides it out again).  With fp16 operands every kernel
-  // scales Q-hat instead, and K-hat goes to sK unscaled in bf16 (the dQ
-  // product's operand) and to sKf in fp16 (times fk in a rescaled pass).
+  // scales Q-hat instead, and K-hat goes to sKf in fp16 (times fk in a
+  // rescaled pass), the operand of both the logits and the dQ products.
   auto put_khat = [&](int off, float (&xk)[8]) __attribute__((always_inline)) {
     if constexpr (!FS) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) xk[e] *= p.scale_log2;
       C::put8(&sK[off], xk);
     } else {
-      C::put8(&sK[off], xk);
       if (rescaled) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) xk[e] *= fk;
@@ -440,7 +472,8 @@ bwd_dq_kernel(const BwdParams p) {
     };
     // dS of key block j from its S / dP, then dQ-hat^T += K-hat^T dS^T:
     auto pq = [&](int j, const f32x4 (&sacc)[QT][2], const f32x4 (&pacc)[QT][2]) __attribute__((always_inline)) {
-      Frag dsf[QT], dsfl[FS ? QT : 1];
+      using DFrag = std::conditional_t<FS, LFrag, Frag>;   // FS: sig dS in fp16
+      DFrag dsf[QT];
 #pragma unroll
       for (int t = 0; t < QT; ++t) {
         float ds[8];
@@ -451,24 +484,32 @@ bwd_dq_kernel(const BwdParams p) {
             ds[4 * h + i] = __builtin_amdgcn_fmed3f(
                                 fast_exp2(FS ? __builtin_fmaf(sacc[t][h][i], fsc, -lse2[t])
                                              : sacc[t][h][i] - lse2[t]), 0.f, 1.f) * pacc[t][h][i];
-        if constexpr (FS)
-          split_bf16x8(ds, dsf[t].v, dsfl[t].v);
-        else
+        if constexpr (FS) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ds[e] *= sig;
+          amax_s = amax8(amax_s, ds);
+          dsf[t].v = to_f16x8(ds);
+        } else {
           dsf[t] = C::make(ds);
+        }
       }
 #pragma unroll
       for (int d = 0; d < DT; ++d) {
         // A = K-hat^T rows 16d.., k-slot e <-> key 32j + 8lg + e (the dS^T order)
-        Frag a;
-        if constexpr (TR)
-          a = C::tr(&sK[tr_offset(32 * j + 8 * lg, 16 * d, LDK, lr)],
-                    &sK[tr_offset(32 * j + 8 * lg + 4, 16 * d, LDK, lr)]);
-        else
-          a = C::lds(&sKt[(16 * d + lr) * LDT + 32 * j + 8 * lg]);
+        if constexpr (FS) {
+          const LFrag a = LC::tr(&sKf[tr_offset(32 * j + 8 * lg, 16 * d, LDK, lr)],
+                                 &sKf[tr_offset(32 * j + 8 * lg + 4, 16 * d, LDK, lr)]);
 #pragma unroll
-        for (int t = 0; t < QT; ++t) {
-          if constexpr (FS) dqacc[t][d] = C::mma(a, dsfl[t], dqacc[t][d]);
-          dqacc[t][d] = C::mma(a, dsf[t], dqacc[t][d]);
+          for (int t = 0; t < QT; ++t) dqacc[t][d] = LC::mma(a, dsf[t], dqacc[t][d]);
+        } else {
+          Frag a;
+          if constexpr (TR)
+            a = C::tr(&sK[tr_offset(32 * j + 8 * lg, 16 * d, LDK, lr)],
+                      &sK[tr_offset(32 * j + 8 * lg + 4, 16 * d, LDK, lr)]);
+          else
+            a = C::lds(&sKt[(16 * d + lr) * LDT + 32 * j + 8 * lg]);
+#pragma unroll
+          for (int t = 0; t < QT; ++t) dqacc[t][d] = C::mma(a, dsf[t], dqacc[t][d]);
         }
       }
     };
@@ -510,7 +551,7 @@ bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const float dj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dsx), 8 * j));
-          const S* kb = &sK[(8 * wave + j) * LDK + XO * lane];
+          const f16* kb = &sKf[(8 * wave + j) * LDK + XO * lane];   // K-hat * fk
 #pragma unroll
           for (int i = 0; i < XO; ++i) o[i] = __builtin_fmaf(dj, (float)kb[i], o[i]);
         }
@@ -524,25 +565,36 @@ bwd_dq_kernel(const BwdParams p) {
     // Operand ranges of this pass over the workgroup; if Q-hat or K-hat
     // reached 2^12, run the tile again with scaled logit operands.
     {
-      const unsigned rq = wave_max_bits(amax_q), rk = wave_max_bits(amax_k);
-      if (lane == 0) sRange[wave] = u32x2{rq, rk};
+      const unsigned rq = wave_max_bits(amax_q), rk = wave_max_bits(amax_k), rs = wave_max_bits(amax_s);
+      if (lane == 0) sRange[wave] = u32x4{rq, rk, rs, 0u};
     }
     lds_barrier();
-    unsigned rq = 0, rk = 0;
+    unsigned rq = 0, rk = 0, rs = 0;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      const u32x2 r = sRange[w];
+      const u32x4 r = sRange[w];
       rq = max(rq, r[0]);
       rk = max(rk, r[1]);
+      rs = max(rs, r[2]);
     }
     const unsigned eq = __builtin_amdgcn_readfirstlane(rq) >> 23;
     const unsigned ek = __builtin_amdgcn_readfirstlane(rk) >> 23;
-    if (!rescaled && (eq >= kF16ExpLimit || ek >= kF16ExpLimit)) {
-      rescaled = true;
-      fq = f16_fit(eq);
-      fk = f16_fit(ek);
-      fsc = 1.f / (fq * fk);
-      amax_q = amax_k = 0.f;
+    const unsigned es = __builtin_amdgcn_readfirstlane(rs) >> 23;
+    // logit operands past 2^12 (once), or sig dS outside [2^-10, 2^15)
+    // (es == 0: every dS is zero); at most three passes
+    const bool redo_l = !rescaled && (eq >= kF16ExpLimit || ek >= kF16ExpLimit);
+    const bool redo_s = es >= 142u || (es != 0u && es < 117u);
+    if ((redo_l || redo_s) && npass < 2) {
+      ++npass;
+      if (redo_l) {
+        rescaled = true;
+        fq = f16_fit(eq);
+        fk = f16_fit(ek);
+        fsc = 1.f / (fq * fk);
+      }
+      // (a max of inf / NaN keeps sig: f16_fit(255) would flush every value)
+      if (redo_s && es < 255u) sig *= f16_fit(es);
+      amax_q = amax_k = amax_s = 0.f;
       continue;
     }
   }
@@ -556,7 +608,7 @@ bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) g4[r] += sXo[w][4 * ln + r];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) g4[r] *= dq_scale;
+      for (int r = 0; r < 4; ++r) g4[r] *= p.scale / fk;   // (K-hat * fk, fp32 dS)
       rope_unrotate4(g4, tab, N - 1 + shift, D2, 2 * ln);
       store4(dQ + (N - 1) * p.sdq[2] + 4 * ln * p.sdq[3], p.sdq[3], p.vec_dq, g4);
     }

@@ -52,13 +52,18 @@ struct BwdParams {
                        // rows of key N - 1 here ([planes][n_blk][2][D] fp32)
   void* qhat_f;        // non-null (fp16 logits): fp16 of Q-hat * scale * log2(e),
                        // [planes][N][D], written by the dQ kernel's first pass and
-                       // staged by the dK/dV kernel
+                       // staged by the dK/dV (or key-tile) kernel
+  float* row_stat;     // non-null: per query row {|dO|_2, max |Q-hat * scale * log2(e)|}
+                       // [planes * N][2], written by the dQ kernel's first pass; the
+                       // key-tile kernel (bwd_keys.hip) then replaces the dK/dV kernel
 };
 
 // Launch shapes picked by the tile table (api.hip).
 enum BwdVariant : int {
   BWD_FUSED = 0,    // one workgroup per plane: dK, dV and dQ in one pass (N <= 256)
   BWD_SPLIT = 1,    // dQ kernel (Q-outer, also writes delta) + dK/dV kernel (KV-outer)
+  BWD_SPLIT16 = 2,  // dQ kernel + key-tile kernel, both with fp16 dS products
+                    // (bwd_keys.hip; with vector access to every tensor, else BWD_SPLIT)
 };
 
 // Launchers: return hipSuccess or the launch error.  io/ct are DT_* codes.
@@ -86,6 +91,13 @@ hipError_t launch_bwd_tail_keys(const BwdParams& p, int io, int D, int key0, hip
 // Key N - 1 from the dQ kernel's per-tile partial rows (p.xk_ws, nparts per
 // plane) instead of launch_bwd_tail_keys; D = 128 or 256, 16-bit I/O.
 hipError_t launch_bwd_tail_key_merge(const BwdParams& p, int io, int D, int nparts, hipStream_t st);
+// Key tiles with fp16 dS products (bwd_keys.hip): dK and dV of p.n_blk
+// 128-key tiles per plane, in place of launch_bwd_dkdv, for 16-bit I/O, bf16
+// compute, head_dim 128 and vector access to every tensor; needs p.qhat_f and
+// p.row_stat (and delta) from the dQ kernel's pass before it.
+constexpr int kKeysRows = 128;
+hipError_t launch_bwd_keys(const BwdParams& p, int io, hipStream_t st);
+
 // Whether the forward block kernel computes a single tail row itself
 // (FwdParams::x_rows = 1) instead of launch_fwd_tail: fp16 logit operands with
 // vector access (vec: every tensor of the call allows it).
