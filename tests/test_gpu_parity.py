@@ -418,29 +418,35 @@ def test_large_logits_finite():
 
 
 @pytest.mark.parametrize("planes", [
-    # (q scale, k scale) per (b, h) plane: 2^20 / 2^-20 push |Q-hat| (with the
-    # logit scale) far past 2^12 and |K-hat| into fp16's subnormal range, and
-    # the reverse makes K-hat overflow fp16; the logits themselves stay those
-    # of unit inputs.  2^11 / 2^-11 stays below the rescale threshold.
-    [(2.0 ** 20, 2.0 ** -20), (1.0, 1.0), (2.0 ** -20, 2.0 ** 20), (2.0 ** 11, 2.0 ** -11)],
-], ids=["mixed"])
+    # (q scale, k scale, v scale) per (b, h) plane: 2^20 / 2^-20 push |Q-hat|
+    # (with the logit scale) far past 2^12 and |K-hat| into fp16's subnormal
+    # range, and the reverse makes K-hat overflow fp16; the logits themselves
+    # stay those of unit inputs.  2^11 / 2^-11 stays below the rescale threshold.
+    [(2.0 ** 20, 2.0 ** -20, 1.0), (1.0, 1.0, 1.0), (2.0 ** -20, 2.0 ** 20, 1.0), (2.0 ** 11, 2.0 ** -11, 1.0)],
+    # V past fp16's range (2^20), deep in its subnormal range (2^-20), and
+    # just past the 2^12 rescale threshold (2^11 x |N(0,1)| up to ~2^13)
+    [(1.0, 1.0, 2.0 ** 20), (1.0, 1.0, 2.0 ** -20), (1.0, 1.0, 1.0), (1.0, 1.0, 2.0 ** 11)],
+], ids=["qk", "v"])
 def test_f16_logit_operand_range(planes):
-    """bf16 compute at head_dim 128 takes the logits from fp16 operands; a tile
-    whose Q-hat or K-hat reaches 2^12 is computed again with both operands
-    rescaled by powers of two.  With Q = a q0, K = k0 / a the logits are those
-    of (q0, k0), O and dV are unchanged, dQ scales by 1/a and dK by a: each
-    plane's outputs, divided by those factors, must meet the north-star
-    tolerance against the fp32 oracle on the same (scaled, bf16) inputs."""
+    """bf16 compute at head_dim 128 takes the logits (and the forward's P V) from
+    fp16 operands; a tile whose Q-hat or K-hat reaches 2^12, or whose V leaves
+    [2^-10, 2^12), is computed again with its operands rescaled by powers of
+    two.  With Q = a q0, K = k0 / a the logits are those of (q0, k0), O and dV
+    are unchanged, dQ scales by 1/a and dK by a; with V = c v0, O, dQ and dK
+    scale by c and dV is unchanged.  Each plane's outputs, divided by those
+    factors, must meet the north-star tolerance against the fp32 oracle on the
+    same (scaled, bf16) inputs."""
     B, H, side, D = 2, 2, 16, 128
     N = side * side + 1
     g = torch.Generator().manual_seed(3)
     q, k, v, do = (torch.randn(B, H, N, D, generator=g) for _ in range(4))
     fac = torch.ones(B, H, 4)
-    for i, (a, c) in enumerate(planes):
+    for i, (a, c, w) in enumerate(planes):
         b, h = divmod(i, H)
         q[b, h] *= a
         k[b, h] *= c
-        fac[b, h] = torch.tensor([1.0, c, a, 1.0])   # O, dQ, dK, dV magnitude factors
+        v[b, h] *= w
+        fac[b, h] = torch.tensor([w, c * w, a * w, 1.0])   # O, dQ, dK, dV magnitude factors
     q, k, v, do = (t.to(torch.bfloat16).to(DEV) for t in (q, k, v, do))
     table = CosSinTable(ROPE_BASE, side, D, device=DEV)
     ours = _run_ours(q, k, v, do, table, True)

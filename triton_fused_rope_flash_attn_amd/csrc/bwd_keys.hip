@@ -40,7 +40,6 @@ namespace farope {
 
 namespace {
 constexpr int kKeysD = 128;
-constexpr unsigned kF16ExpLow = 117;   // biased fp32 exponent of 2^-10
 
 template <typename IO>
 __device__ __forceinline__ const IO* plane_ptr(const void* b, const int64_t* st, int plane, int H) {

@@ -439,6 +439,7 @@ __device__ __forceinline__ void split_bf16x8(const float (&x)[8], bf16x8& hi, bf
 // Otherwise the scales are 1 and the factor is exact.
 // ---------------------------------------------------------------------------
 constexpr unsigned kF16ExpLimit = 139;   // biased fp32 exponent of 2^12
+constexpr unsigned kF16ExpLow = 117;     // biased fp32 exponent of 2^-10
 
 // running max of |x| over 8 values (NaN is ignored)
 __device__ __forceinline__ float amax8(float a, const float (&x)[8]) {

@@ -82,8 +82,12 @@ constexpr float kRescaleSlack = 8.0f;   // log2 units: P <= 2^8 between rescales
 // FS (bf16 compute): the logits product takes fp16 operands (K-hat tile in
 // LDS, Q-hat fragments in registers): the rounding of the rotated rows to
 // bf16 is what dominates the error of bf16 attention at long, wide planes.
-// P and V stay bf16.  An item whose Q-hat or K-hat reaches 2^12 is computed
-// again with scaled operands (f16_fit in common.h).
+// O = P V takes fp16 P and V too (V times fv; bf16 values convert exactly
+// inside fp16's range): with bf16 P, O's computation error (2^-9 per
+// probability) was as large as its storage rounding, and the backward's
+// delta = rowsum(dO * O) inherits it.  An item whose Q-hat or K-hat reaches
+// 2^12, or whose V leaves [2^-10, 2^12), is computed again with scaled
+// operands (f16_fit in common.h).
 template <typename IO, int CT, int D, int NW, int QT, int KC, int TABROWS, bool VEC, bool FS>
 __global__ void __launch_bounds__(NW * 64)
 fwd_kernel(const FwdParams p) {
@@ -92,6 +96,9 @@ fwd_kernel(const FwdParams p) {
   using Frag = typename C::Frag;
   using LC = std::conditional_t<FS, Comp<DT_F16>, C>;   // logits operands
   using LFrag = typename LC::Frag;
+  using VC = std::conditional_t<FS, Comp<DT_F16>, C>;   // P and V operands
+  using VS = typename VC::S;
+  using VFrag = typename VC::Frag;
   constexpr int KS = D / 32;          // k-steps of 32 channels
   constexpr int DT = D / 16;          // 16-channel output subtiles
   constexpr int D2 = D / 2;
@@ -118,8 +125,8 @@ fwd_kernel(const FwdParams p) {
   static_assert(!FS || CT == DT_BF16, "fp16 logit operands go with bf16 compute");
   __shared__ __attribute__((aligned(16))) S sK[2][KC * LDK];   // FS: fp16 K-hat
   // FS: per-wave max |Q-hat|, max |K-hat| bit patterns of an item pass
-  __shared__ u32x2 sRange[FS ? NW : 1];
-  __shared__ __attribute__((aligned(16))) S sVt[2][(TRV || VROW) ? KC * LDK : D * LDV];
+  __shared__ u32x4 sRange[FS ? NW : 1];
+  __shared__ __attribute__((aligned(16))) VS sVt[2][(TRV || VROW) ? KC * LDK : D * LDV];
   // XR: the plane's last row, when it is the only one past the full query
   // blocks (p.x_rows == 1, N = 1 + a multiple of the block rows), rides along
   // one designated item of the plane instead of a tail kernel that would read
@@ -201,9 +208,13 @@ fwd_kernel(const FwdParams p) {
   // current pass of an item; the operand scales and the logit factor
   // 1 / (fq fk) of a rescaled pass (all 1 otherwise).
   float amax_q = 0.f, amax_k = 0.f;
-  float fq = 1.f, fk = 1.f, fsc = 1.f;
+  typedef unsigned short vu16x2 __attribute__((ext_vector_type(2)));
+  vu16x2 amax_vb = {0, 0};   // FS: largest |V| bit patterns (16-bit I/O) of the pass, two lanes
+  float amax_vf = 0.f;       // FS: largest |V * fv| (32-bit I/O) of the pass
+  float fq = 1.f, fk = 1.f, fsc = 1.f, fv = 1.f;
+  float ifv = 1.f;   // 1 / fv of the item's kept pass (O comes out times fv)
   bool rescaled = false, redo = false;
-  unsigned eq = 0, ek = 0;   // biased exponents of the pass's max |Q-hat|, |K-hat|
+  unsigned eq = 0, ek = 0, ev = 0;   // biased exponents of the pass's max |Q-hat|, |K-hat|, |V|
 
   // ---- KV chunk prefetch registers: two rows x 8 channels of K and V
   //      (+ their cos/sin when the table is not in LDS) ----
@@ -327,7 +338,27 @@ fwd_kernel(const FwdParams p) {
           } else {
             C::put8(&sK[slot][kperm(2 * rp + x) * LDK + 8 * cc], xk);
           }
-          if constexpr (TRV || VROW) {
+          if constexpr (FS) {
+            // V in fp16, times fv (1 except in a rescaled pass); its range
+            // from the raw 16-bit patterns (|x| orders like its bits without
+            // the sign), two per packed integer max
+            float y[8];
+            unpack8(pv[it][x], y);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) y[e] *= fv;
+            if constexpr (sizeof(IO) == 2) {
+              u32x4 w;
+              __builtin_memcpy(&w, &pv[it][x].v, 16);
+              vu16x2 m = __builtin_bit_cast(vu16x2, w[0] & 0x7fff7fffu);
+#pragma unroll
+              for (int k = 1; k < 4; ++k)
+                m = __builtin_elementwise_max(m, __builtin_bit_cast(vu16x2, w[k] & 0x7fff7fffu));
+              amax_vb = opaque_vec(__builtin_elementwise_max(amax_vb, m));
+            } else {
+              amax_vf = opaque(amax8(amax_vf, y));
+            }
+            *reinterpret_cast<f16x8*>(&sVt[slot][vrow(2 * rp + x) * LDK + 8 * cc]) = to_f16x8(y);
+          } else if constexpr (TRV || VROW) {
             S* dst = &sVt[slot][vrow(2 * rp + x) * LDK + 8 * cc];
             if constexpr (std::is_same<IO, S>::value) {
               *reinterpret_cast<typename Raw8<IO>::vec*>(dst) = pv[it][x].v;   // raw row segment
@@ -453,7 +484,7 @@ fwd_kernel(const FwdParams p) {
   // Lane (key kk = lane / 8, slice ds = lane % 8) forms the fp16 dot product
   // over channels D/8 * ds .. of its key; then every lane updates channels
   // XO * lane .. of the wave's partial O with the 8 probabilities.
-  auto xrow_chunk = [&](const S* __restrict__ cK, const S* __restrict__ cV, int kvb, bool first)
+  auto xrow_chunk = [&](const S* __restrict__ cK, const VS* __restrict__ cV, int kvb, bool first)
       __attribute__((always_inline)) {
     // (lane addresses from an opaque copy: recomputed here, not kept live
     // through the chunk loop)
@@ -485,7 +516,7 @@ fwd_kernel(const FwdParams p) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pk), 8 * j));
-      const S* vp = cV + vrow(8 * wave + j) * LDK + XO * ln;
+      const VS* vp = cV + vrow(8 * wave + j) * LDK + XO * ln;
 #pragma unroll
       for (int i = 0; i < XO; ++i) o[i] = __builtin_fmaf(pj, (float)vp[i], o[i]);
     }
@@ -516,7 +547,7 @@ fwd_kernel(const FwdParams p) {
   // SIMDs that would otherwise wait at the next barrier.
   // VROW: V^T fragment (rows 16d.., k-slot e <-> key 32j + 8lg + e) gathered
   // from the row-major V tile, one element per key row.
-  auto vrow_frag = [&](const S* __restrict__ cV, int j, int d) __attribute__((always_inline)) {
+  auto vrow_frag = [&](const VS* __restrict__ cV, int j, int d) __attribute__((always_inline)) {
     float x[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = (float)cV[(32 * j + 8 * lg + e) * LDK + 16 * d + lr];
@@ -524,7 +555,7 @@ fwd_kernel(const FwdParams p) {
   };
   using SAcc = f32x4[QT][2];
   using KFr = Frag[KS][2];
-  using VFr = Frag[DT];
+  using VFr = VFrag[DT];
   // K-hat fragments of block j: key kv = 8*(r/4) + 4*h + r%4 in A-row r of half h
   auto load_k = [&](const S* __restrict__ cK, int j, KFr& kf) __attribute__((always_inline)) {
 #pragma unroll
@@ -533,11 +564,11 @@ fwd_kernel(const FwdParams p) {
       for (int h = 0; h < 2; ++h) kf[s][h] = C::lds(&cK[(32 * j + 16 * h + lr) * LDK + 32 * s + 8 * lg]);
   };
   // V^T fragments of block j: A = V^T rows 16d.., k-slot e <-> key 32j + 8lg + e (the P^T order)
-  auto load_v = [&](const S* __restrict__ cV, int j, VFr& vf) __attribute__((always_inline)) {
+  auto load_v = [&](const VS* __restrict__ cV, int j, VFr& vf) __attribute__((always_inline)) {
 #pragma unroll
     for (int d = 0; d < DT; ++d) {
       if constexpr (TRV)
-        vf[d] = C::tr(cV + (32 * j + vr0) * LDK + 16 * d + 4 * (lr & 3),
+        vf[d] = VC::tr(cV + (32 * j + vr0) * LDK + 16 * d + 4 * (lr & 3),
                       cV + (32 * j + vr1) * LDK + 16 * d + 4 * (lr & 3));
       else if constexpr (VROW)
         vf[d] = vrow_frag(cV, j, d);
@@ -586,16 +617,19 @@ fwd_kernel(const FwdParams p) {
     return fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
   };
   // sv: logits minus the running max (the seeded accumulators)
-  auto probs = [&](const float (&sv)[8], int t, Frag& pft) __attribute__((always_inline)) {
+  auto probs = [&](const float (&sv)[8], int t, VFrag& pft) __attribute__((always_inline)) {
     float pv8[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       pv8[e] = fast_exp2(sv[e]);
       l_run[t] += pv8[e];
     }
-    pft = C::make(pv8);
+    if constexpr (FS)
+      pft.v = to_f16x8(pv8);
+    else
+      pft = C::make(pv8);
   };
-  auto soft = [&](auto maskc, const SAcc& sa, int lim, Frag (&pf)[QT], float (&lkeep)[QT]) __attribute__((always_inline)) {
+  auto soft = [&](auto maskc, const SAcc& sa, int lim, VFrag (&pf)[QT], float (&lkeep)[QT]) __attribute__((always_inline)) {
     bool need = false;
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
@@ -609,7 +643,7 @@ fwd_kernel(const FwdParams p) {
   };
   // The new base also applies to a block whose logits are already issued
   // (pend): its accumulators are shifted by the change.
-  auto fixup = [&](auto maskc, const SAcc& sa, int lim, Frag (&pf)[QT], const float (&lkeep)[QT],
+  auto fixup = [&](auto maskc, const SAcc& sa, int lim, VFrag (&pf)[QT], const float (&lkeep)[QT],
                    SAcc* pend) __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
@@ -635,20 +669,20 @@ fwd_kernel(const FwdParams p) {
       }
     }
   };
-  auto softmax = [&](auto maskc, const SAcc& sa, int lim, Frag (&pf)[QT], SAcc* pend) __attribute__((always_inline)) {
+  auto softmax = [&](auto maskc, const SAcc& sa, int lim, VFrag (&pf)[QT], SAcc* pend) __attribute__((always_inline)) {
     float lkeep[QT];
     if (soft(maskc, sa, lim, pf, lkeep)) fixup(maskc, sa, lim, pf, lkeep, pend);
   };
   // O^T += V^T P^T (each V^T fragment feeds QT MFMAs)
-  auto out_mma = [&](const VFr& vf, const Frag (&pf)[QT]) __attribute__((always_inline)) {
+  auto out_mma = [&](const VFr& vf, const VFrag (&pf)[QT]) __attribute__((always_inline)) {
 #pragma unroll
     for (int d = 0; d < DT; ++d)
 #pragma unroll
-      for (int t = 0; t < QT; ++t) oacc[t][d] = C::mma(vf[d], pf[t], oacc[t][d]);
+      for (int t = 0; t < QT; ++t) oacc[t][d] = VC::mma(vf[d], pf[t], oacc[t][d]);
   };
   // One KV chunk of nb blocks; the block holding key N-1 is the last one of
   // the chunk that starts at kvb (the ragged chunk is processed first).
-  auto chunk = [&](const S* __restrict__ cK, const S* __restrict__ cV, int kvb, bool active, auto&& mem) __attribute__((always_inline)) {
+  auto chunk = [&](const S* __restrict__ cK, const VS* __restrict__ cV, int kvb, bool active, auto&& mem) __attribute__((always_inline)) {
     const int nkeys = min(KC, N - kvb);
     // a wave with no query row below N runs one block (its results are never
     // stored) so that every wave reaches mem() on the same straight-line path
@@ -656,7 +690,7 @@ fwd_kernel(const FwdParams p) {
     SAcc s0, s1;
     KFr ka, kb;
     VFr vf;
-    Frag pf[QT];
+    VFrag pf[QT];
     load_k(cK, 0, ka);
     logits(ka, s0);
     load_k(cK, min(1, nb - 1), kb);
@@ -732,12 +766,12 @@ fwd_kernel(const FwdParams p) {
       }
     }
   };
-  auto blk_out = [&](auto maskc, const S* __restrict__ cV, int kvb, int j, const SAcc& sacc)
+  auto blk_out = [&](auto maskc, const VS* __restrict__ cV, int kvb, int j, const SAcc& sacc)
       __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(maskc)::value;
     // ---- online softmax; lane holds keys kvb + 32j + 8lg + (0..7) of its row ----
     const int lim = N - (kvb + 32 * j + 8 * lg);   // keys e < lim are valid (MASKED only)
-    Frag pf[QT];
+    VFrag pf[QT];
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
       float sv[8];
@@ -773,21 +807,24 @@ fwd_kernel(const FwdParams p) {
         pv8[e] = fast_exp2(FS ? __builtin_fmaf(sv[e], fsc, -m_run[t]) : sv[e] - m_run[t]);
         l_run[t] += pv8[e];
       }
-      pf[t] = C::make(pv8);
+      if constexpr (FS)
+        pf[t].v = to_f16x8(pv8);
+      else
+        pf[t] = C::make(pv8);
     }
     // ---- O^T += V^T P^T (each V^T fragment feeds QT MFMAs) ----
 #pragma unroll
     for (int d = 0; d < DT; ++d) {
       // A = V^T rows 16d.., k-slot e <-> key 32j + 8lg + e (the P^T order)
-      Frag a;
+      VFrag a;
       if constexpr (TRV)
-        a = C::tr(cV + (32 * j + vr0) * LDK + 16 * d + 4 * (lr & 3), cV + (32 * j + vr1) * LDK + 16 * d + 4 * (lr & 3));
+        a = VC::tr(cV + (32 * j + vr0) * LDK + 16 * d + 4 * (lr & 3), cV + (32 * j + vr1) * LDK + 16 * d + 4 * (lr & 3));
       else if constexpr (VROW)
         a = vrow_frag(cV, j, d);
       else
         a = C::lds(&cV[(16 * d + lr) * LDV + vswz(16 * d + lr, 32 * j + 8 * lg)]);
 #pragma unroll
-      for (int t = 0; t < QT; ++t) oacc[t][d] = C::mma(a, pf[t], oacc[t][d]);
+      for (int t = 0; t < QT; ++t) oacc[t][d] = VC::mma(a, pf[t], oacc[t][d]);
     }
   };
   // One KV chunk of nb blocks (the last one ragged when N - kvb < KC and not
@@ -796,7 +833,7 @@ fwd_kernel(const FwdParams p) {
   // before the softmax of block j, so that those MFMAs run while the VALU
   // computes block j's probabilities; two blocks per trip alternate the two
   // logit accumulators without copies.
-  auto chunk_serial = [&](const S* __restrict__ cK, const S* __restrict__ cV, int kvb) __attribute__((always_inline)) {
+  auto chunk_serial = [&](const S* __restrict__ cK, const VS* __restrict__ cV, int kvb) __attribute__((always_inline)) {
     const int nkeys = min(KC, N - kvb);
     if constexpr (sizeof(S) == 2 && (QT == 1 || (VEC && D >= 128))) {
       // every block goes through the masked softmax (a key limit past the
@@ -957,20 +994,30 @@ fwd_kernel(const FwdParams p) {
         // once more.
         if (c == nch - 1) {
           {
-            const unsigned rq = wave_max_bits(amax_q), rk = wave_max_bits(amax_k);
-            if (lane == 0) sRange[wave] = u32x2{rq, rk};
+            // |V| of the raw 16-bit patterns as fp32 (bf16: the top half of an
+            // fp32; fp16: converted) for the wave maximum
+            const unsigned short vb = max(amax_vb[0], amax_vb[1]);
+            float va = amax_vf;
+            if constexpr (std::is_same<IO, bf16>::value) va = __uint_as_float((unsigned)vb << 16) * fv;
+            if constexpr (std::is_same<IO, f16>::value) va = (float)__builtin_bit_cast(f16, vb) * fv;
+            const unsigned rq = wave_max_bits(amax_q), rk = wave_max_bits(amax_k), rv = wave_max_bits(va);
+            if (lane == 0) sRange[wave] = u32x4{rq, rk, rv, 0u};
           }
           lds_barrier();
-          unsigned rq = 0, rk = 0;
+          unsigned rq = 0, rk = 0, rv = 0;
 #pragma unroll
           for (int w = 0; w < NW; ++w) {
-            const u32x2 r = sRange[w];
+            const u32x4 r = sRange[w];
             rq = max(rq, r[0]);
             rk = max(rk, r[1]);
+            rv = max(rv, r[2]);
           }
           eq = __builtin_amdgcn_readfirstlane(rq) >> 23;
           ek = __builtin_amdgcn_readfirstlane(rk) >> 23;
-          redo = !rescaled && (eq >= kF16ExpLimit || ek >= kF16ExpLimit);
+          ev = __builtin_amdgcn_readfirstlane(rv) >> 23;
+          // (ev == 0: V is zero, nothing to resolve)
+          redo = !rescaled && (eq >= kF16ExpLimit || ek >= kF16ExpLimit || ev >= kF16ExpLimit ||
+                               (ev != 0u && ev < kF16ExpLow));
         }
       }
       if constexpr (FIRST && kPipe) flush_o();
@@ -1013,7 +1060,8 @@ fwd_kernel(const FwdParams p) {
     if constexpr (FS) {
       // a rescaled second pass (its first chunk is already on the way; no
       // Q prefetch or deferred store exists with these operands); no store
-      amax_q = amax_k = 0.f;
+      amax_q = amax_k = amax_vf = 0.f;
+      amax_vb = vu16x2{0, 0};
       if constexpr (XR) ++npass;
       if (redo) {
         redo = false;
@@ -1021,10 +1069,12 @@ fwd_kernel(const FwdParams p) {
         fq = f16_fit(eq);
         fk = f16_fit(ek);
         fsc = 1.f / (fq * fk);
+        fv = ev != 0u ? f16_fit(ev) : 1.f;
         continue;
       }
+      ifv = 1.f / fv;
       rescaled = false;
-      fq = fk = fsc = 1.f;
+      fq = fk = fsc = fv = 1.f;
     }
     if constexpr (XR) {
       if (xi) {
@@ -1044,7 +1094,7 @@ fwd_kernel(const FwdParams p) {
 #pragma unroll
             for (int i = 0; i < XO; ++i) o[i] = __builtin_fmaf(sXo[w][XO * ln + i], a, o[i]);
           }
-          const float inv = 1.f / L;
+          const float inv = ifv / L;
           IO* orow_p = const_cast<IO*>(plane_base(p.o, p.so, plane)) + (N - 1) * p.so[2] + XO * ln;
           typedef IO iox __attribute__((ext_vector_type(XO)));
           iox h, rr;
@@ -1104,7 +1154,7 @@ fwd_kernel(const FwdParams p) {
       for (int t = 0; t < QT; ++t) {
         const float l = group4_sum(l_run[t]);
         const int row = (qb * NW * QT + t * NW + wave) * 16 + lr;
-        const float inv = __builtin_amdgcn_rcpf(l);
+        const float inv = __builtin_amdgcn_rcpf(l) * ifv;
 #pragma unroll
         for (int d = 0; d < DT; ++d) {
           float o4[4];
@@ -1133,7 +1183,7 @@ fwd_kernel(const FwdParams p) {
         const float l = group4_sum(l_run[t]);
         const int row = (qb * NW * QT + t * NW + wave) * 16 + lr;
         if (t < nt && row < N) {
-          const float inv = __builtin_amdgcn_rcpf(l);
+          const float inv = __builtin_amdgcn_rcpf(l) * ifv;
 #pragma unroll
           for (int d = 0; d < DT; ++d) {
             float o4[4];
