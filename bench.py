@@ -436,7 +436,8 @@ def main():
     desc = _lib.make_desc(B, H, N, D, n_pos, wl["has_cls"], _lib.BF16, _lib.BF16, scale)
     bwd_cfg = _lib.tile_config(desc, 1)
     fwd_cfg = _lib.tile_config(desc, 0)
-    bwd_kernel = "bwd_plane_kernel" if bwd_cfg[0] == 0 else "bwd_dq_kernel + bwd_dkdv_kernel"
+    bwd_kernel = {0: "bwd_plane_kernel", 1: "bwd_dq_kernel + bwd_dkdv_kernel",
+                  2: "bwd_dq_kernel + bwd_keys_kernel"}[bwd_cfg[0]]
 
     traffic = None
     if os.path.exists(TRAFFIC_FILE):

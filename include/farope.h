@@ -116,7 +116,11 @@ size_t farope_attn_residual_elems(const farope_attn_desc* desc);
  * then, at those fp16-logit shapes whenever every row lies in a dQ tile,
  * batch * heads * seq_len * head_dim fp16 values (from a 256-byte boundary):
  * the dQ pass's rotated Q rows, which the dK/dV pass stages instead of
- * rotating Q again for every key tile.  0 on an invalid descriptor.
+ * rotating Q again for every key tile; then, of those shapes at head_dim
+ * 128, 2 * batch * heads * seq_len fp32 values (from a 256-byte boundary):
+ * each query row's {|dO|_2, max |Q-hat * scale * log2(e)|}, from which the
+ * key-tile kernel fixes its fp16 operand scalings.  0 on an invalid
+ * descriptor.
  */
 size_t farope_attn_bwd_workspace_elems(const farope_attn_desc* desc);
 
@@ -192,12 +196,14 @@ int farope_attn_bwd(const farope_attn_desc* desc,
  * lives in a static device array of FAROPE_NOALLOC_MAX_ROWS fp32 values that
  * the library holds on every device it runs on until the process ends; calls
  * that need more return FAROPE_ERR_SCRATCH before anything is launched.  The
- * rotated Q rows of farope_attn_bwd_workspace_elems go there too when the
- * whole workspace fits; otherwise the dK/dV pass rotates Q itself (results
- * within rounding of farope_attn_bwd's).  Allocates nothing.  Calls on one device share that array, so
- * calls that overlap on one device (concurrent streams or threads) race;
- * calls ordered on one stream do not.  The current device must be the one
- * holding the tensors.
+ * rotated Q rows and row statistics of farope_attn_bwd_workspace_elems go
+ * there too when the whole workspace fits, and the kernels are then those of
+ * farope_attn_bwd; otherwise the generic dK/dV kernel runs and rotates Q
+ * itself (results within rounding of farope_attn_bwd's).  The one-pass
+ * backward uses no workspace and takes any size.  Allocates nothing.  Calls
+ * on one device share that array, so calls that overlap on one device
+ * (concurrent streams or threads) race; calls ordered on one stream do not.
+ * The current device must be the one holding the tensors.
  */
 int farope_attn_bwd_noalloc(const farope_attn_desc* desc,
                             const void* q, const int64_t q_stride[4],
