@@ -94,12 +94,13 @@ int farope_rope_pack(const float* cosp, int64_t cos_stride0, int64_t cos_stride1
 /*
  * Elements of the optional O residual buffer (o_res) a call uses:
  * batch * heads * seq_len * head_dim for bf16 tensors computed in bf16 at
- * head_dim >= 128, else 0.  Those calls take the logits from split bf16
- * operands; what then limits dQ / dK is delta = rowsum(dout * o) computed
- * from the bf16-rounded o, so the forward can also store o's rounding
- * residual bf16(o - bf16(o)) in a contiguous [B, H, N, D] buffer of the I/O
- * dtype, and the backward adds it to o for delta.  No counterpart in the
- * reference (whose delta uses the stored o, FA:352-354).
+ * head_dim >= 128, else 0.  Those calls take the logits, O = P V and the dQ /
+ * dK products from fp16 operands; delta = rowsum(dout * o) taken from the
+ * bf16-rounded o would then be the largest error term of dQ / dK, so the
+ * forward can also store o's rounding residual bf16(o - bf16(o)) in a
+ * contiguous [B, H, N, D] buffer of the I/O dtype, and the backward adds it
+ * to o for delta.  No counterpart in the reference (whose delta uses the
+ * stored o, FA:352-354).
  */
 size_t farope_attn_residual_elems(const farope_attn_desc* desc);
 
