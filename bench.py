@@ -470,7 +470,8 @@ def main():
         },
         "pct_mfma_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
         "roofline_fraction_fwd_bwd": round((tf_star + tb_star) / dt, 4),
-        "fwd": {"ms": round(t_fwd * 1e3, 4), "tflops": round(f_fwd / t_fwd / 1e12, 2),
+        "fwd": {"kernel": {0: "fwd_kernel", 1: "fwd_plane_kernel"}[fwd_cfg[0]],
+                "ms": round(t_fwd * 1e3, 4), "tflops": round(f_fwd / t_fwd / 1e12, 2),
                 "gbs": round(by_fwd / t_fwd / 1e9, 1), "roofline_fraction": round(tf_star / t_fwd, 4),
                 "tile": fwd_cfg},
         "bwd": {"ms": round(t_bwd * 1e3, 4), "tflops": round(f_bwd / t_bwd / 1e12, 2),

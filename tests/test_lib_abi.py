@@ -64,15 +64,17 @@ def test_rope_packed_elems(lib):
 
 
 @pytest.mark.parametrize(
-    "N,D,has_cls,fwd_items,bwd_var",
-    [(197, 64, 1, 1, 0), (256, 64, 0, 1, 0), (257, 64, 1, 1, 1), (1025, 128, 1, 4, 2), (197, 128, 1, 1, 2),
-     (197, 256, 1, 3, 1), (257, 256, 1, 4, 1), (1100, 128, 1, 5, 2)],
+    "N,D,has_cls,fwd_var,fwd_items,bwd_var",
+    [(197, 64, 1, 1, 1, 0), (208, 64, 0, 1, 1, 0), (192, 64, 1, 0, 1, 0), (256, 64, 0, 0, 1, 0),
+     (257, 64, 1, 0, 1, 1), (1025, 128, 1, 0, 4, 2), (197, 128, 1, 0, 1, 2),
+     (197, 256, 1, 0, 3, 1), (257, 256, 1, 0, 4, 1), (1100, 128, 1, 0, 5, 2)],
 )
-def test_tile_table(lib, N, D, has_cls, fwd_items, bwd_var):
+def test_tile_table(lib, N, D, has_cls, fwd_var, fwd_items, bwd_var):
+    """Forward variant 1 (one wave per plane) covers planes of 193 .. 208 tokens at D = 64."""
     desc = _lib.make_desc(8, 12, N, D, N - has_cls, has_cls, _lib.BF16, _lib.BF16, D ** -0.5)
     f = _lib.tile_config(desc, 0)
     b = _lib.tile_config(desc, 1)
-    assert f[0] == 0 and f[2] == fwd_items and b[0] == bwd_var
+    assert f[0] == fwd_var and f[2] == fwd_items and b[0] == bwd_var
     for t in (f, b):
         left = N - t[1] * t[2]               # rows for the tail kernels (at most 8)
         assert left <= 8 and t[2] >= 1

@@ -20,7 +20,11 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 INCLUDE = os.path.join(REPO_DIR, "include")
 LIB_NAME = "libfarope.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["api.hip", "fwd.hip", "bwd.hip", "bwd_fused.hip", "bwd_keys.hip", "tail.hip"]
+SOURCES = ["api.hip", "fwd.hip", "fwd_plane.hip", "bwd.hip", "bwd_fused.hip", "bwd_keys.hip", "tail.hip"]
+# Per-file code generation options.  fwd_plane.hip keeps its MFMA results in
+# VGPRs (they feed the softmax VALU directly) and its resident operand
+# fragments in AGPRs.
+EXTRA_FLAGS = {"fwd_plane.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 ARCH = "gfx950"
 
 
@@ -71,7 +75,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
         for src in SOURCES:
             obj = os.path.join(tmp, src.replace(".hip", ".o"))
             objs.append(obj)
-            cmds.append([hipcc, *flags, "-c", os.path.join(CSRC, src), "-o", obj])
+            cmds.append([hipcc, *flags, *EXTRA_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj])
         jobs = jobs or min(len(cmds), os.cpu_count() or 1, 16)
         with _cf.ThreadPoolExecutor(max_workers=jobs) as ex:
             for cmd, fut in zip(cmds, [ex.submit(_run, c) for c in cmds]):

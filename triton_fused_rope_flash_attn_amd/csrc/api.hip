@@ -119,6 +119,12 @@ bool bwd_fused(const farope_attn_desc* d) {
   return d->head_dim == 64 && d->seq_len <= bwd_fused_rows() && d->compute_dtype != FAROPE_F32;
 }
 
+// The plane forward (fwd_plane.hip): one wave per ViT-sized plane, when every
+// tensor allows vector access (tile_config, which sees no tensors, assumes it).
+bool fwd_plane(const farope_attn_desc* d, bool vec) {
+  return fwd_plane_ok(d->io_dtype, d->compute_dtype, d->head_dim, d->seq_len, d->has_cls, vec);
+}
+
 int cdiv(int a, int b) { return (a + b - 1) / b; }
 
 int fill_common(BwdParams& p, const farope_attn_desc* d, const float* rope) {
@@ -387,6 +393,13 @@ int farope_tile_config(const farope_attn_desc* desc, int32_t which, int32_t out[
   if (!out) return FAROPE_ERR_NULL;
   const int D = desc->head_dim, N = desc->seq_len;
   if (which == 0) {
+    if (fwd_plane(desc, true)) {
+      out[0] = 1;
+      out[1] = fwd_plane_rows();
+      out[2] = 1;
+      out[3] = fwd_plane_threads();
+      return FAROPE_OK;
+    }
     const int rows = fwd_block_rows(D, desc->io_dtype, desc->compute_dtype);
     out[0] = 0;
     out[1] = rows;
@@ -439,13 +452,19 @@ int farope_attn_fwd(const farope_attn_desc* desc, const void* q, const int64_t q
   p.vec_k = vec_ok(k, k_stride, es, desc->seq_len, desc->head_dim);
   p.vec_v = vec_ok(v, v_stride, es, desc->seq_len, desc->head_dim);
   p.vec_o = vec_out_ok(o, o_stride, es, desc->seq_len, desc->head_dim);
+  const bool vec = p.vec_q && p.vec_k && p.vec_v && p.vec_o;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (fwd_plane(desc, vec)) {
+    p.n_blk = 1;
+    p.n_items = p.B * p.H;
+    p.x_rows = 0;
+    return launch_rc(launch_fwd_plane(p, desc->io_dtype, st));
+  }
   const int rows = fwd_block_rows(desc->head_dim, desc->io_dtype, desc->compute_dtype);
   const int tail = tail_of(p.B * p.H, p.N, rows);
   p.n_blk = main_blocks(p.B * p.H, p.N, rows);
   p.n_items = p.B * p.H * p.n_blk;
-  const bool vec = p.vec_q && p.vec_k && p.vec_v && p.vec_o;
   p.x_rows = tail == 1 && fwd_folds_tail(desc->io_dtype, desc->compute_dtype, desc->head_dim, vec);
-  const hipStream_t st = static_cast<hipStream_t>(stream);
   FAROPE_TRY(launch_rc(launch_fwd(p, desc->io_dtype, desc->compute_dtype, desc->head_dim, st)));
   if (tail && !p.x_rows)
     FAROPE_TRY(launch_rc(launch_fwd_tail(p, desc->io_dtype, desc->head_dim, p.N - tail, st)));

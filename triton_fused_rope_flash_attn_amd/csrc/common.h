@@ -173,6 +173,15 @@ __device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, unsigned vo
   }
 }
 
+// 16 bytes per lane from a buffer straight into LDS (buffer_load_dwordx4 ...
+// lds): the wave's 64 x 16 bytes land at lds + 16 * lane.  The LDS address
+// (M0) must be wave-uniform.  Like any buffer load, lanes outside the range
+// read zeros.  (A plain function: referenced from a kernel template, the
+// builtin would keep the host pass from emitting that kernel's launch stub.)
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, void* lds, unsigned voff, unsigned soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+
 // ---------------------------------------------------------------------------
 // RoPE.  The packed table is fp32 [(n_pos + 1)][D/2][2] = (cos, sin) per pair;
 // row 0 is the identity (cos 1, sin 0) and serves the CLS token, so token s

@@ -78,6 +78,15 @@ hipError_t launch_rope_pack(const float* cosp, int64_t cs0, int64_t cs1, const f
                             int64_t ss0, int64_t ss1, int n_pos, int d2, float* out,
                             hipStream_t st);
 
+// Forward for ViT-sized planes (fwd_plane.hip): one wave per (b, h) plane
+// with the plane's K-hat and V^T held in registers.  fwd_plane_ok: 16-bit
+// I/O with the same compute type, head_dim 64, 193 <= N <= 208 and vector
+// access to every tensor.  Covers whole planes (no tail rows).
+bool fwd_plane_ok(int io, int ct, int D, int N, int has_cls, bool vec);
+int fwd_plane_rows();
+int fwd_plane_threads();
+hipError_t launch_fwd_plane(const FwdParams& p, int io, hipStream_t st);
+
 // Tail rows (tail.hip): when 0 < N % block_rows <= kTailMaxRows and N >= block_rows,
 // the block kernels cover the full blocks only and these kernels compute the
 // last tail_rows(N, block_rows) rows (forward: O, LSE; rows: dQ and, with
