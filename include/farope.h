@@ -220,10 +220,11 @@ int farope_attn_bwd_noalloc(const farope_attn_desc* desc,
 /*
  * Tile table query (replaces the reference's triton.autotune configs,
  * FA:76-90, FA:318-324, FA:359-373, FA:693-707).  which: 0 = forward,
- * 1 = backward.  out[0] = variant (fwd: 0 = persistent pipelined kernel;
- * bwd: 0 fused, 1 split), out[1] = query (fwd) or key (bwd) rows per work
- * item, out[2] = work items per (b, h) plane, out[3] = threads per
- * workgroup.  When 1 to 8 rows are left past out[1] * out[2] (N = 1025 with
+ * 1 = backward.  out[0] = variant (fwd: 0 = persistent pipelined kernel,
+ * 1 = one wave per (b, h) plane for 193 <= N <= 208 at head_dim 64 with
+ * 16-bit tensors, assuming vector access; bwd: 0 fused, 1 split, 2 split with
+ * the key-tile kernel), out[1] = query (fwd) or key (bwd) rows per work item,
+ * out[2] = work items per (b, h) plane, out[3] = threads per workgroup.  When 1 to 8 rows are left past out[1] * out[2] (N = 1025 with
  * 128- or 256-row items), they are computed by the tail-row kernels (or, for
  * a single row with fp16 logit operands, by one designated item of each plane
  * in the forward and dQ block kernels) rather than by one more, nearly
