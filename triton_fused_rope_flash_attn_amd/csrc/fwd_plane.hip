@@ -247,6 +247,10 @@ __global__ void __launch_bounds__(kFpW * 64) fwd_plane_kernel(const FwdParams p)
   const int stride = p.n_wg * kFpW;
   if (plane >= planes) return;   // (wave-uniform; no barrier follows)
   Frag vt[4][KS], kf[KT][2];
+  Frag ones;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) C::set(ones, e, 1.f);
+  ones.v = in_agpr(ones.v);
   Raw8<IO> qr[KT][2], kr[KT][2];
   // Q rows of subtiles t + 2 .. t + kQpf - 1 are in flight while subtile t runs
   constexpr int kQpf = 5;
@@ -285,7 +289,7 @@ __global__ void __launch_bounds__(kFpW * 64) fwd_plane_kernel(const FwdParams p)
     // probabilities as B-operand fragments of O^T += V^T P^T (k-slot e of
     // step j: tile 2j, i = e for e < 4; tile 2j + 1, i = e - 4 otherwise),
     // row max m and row sum l
-    auto softmax = [&](f32x4 (&sc)[KT], Frag (&pf)[KS], float& m, float& l) __attribute__((always_inline)) {
+    auto softmax = [&](f32x4 (&sc)[KT], Frag (&pf)[KS], float& m) __attribute__((always_inline)) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         if (i >= klim) sc[KT - 1][i] = -__builtin_inff();
@@ -296,16 +300,11 @@ __global__ void __launch_bounds__(kFpW * 64) fwd_plane_kernel(const FwdParams p)
         m1 = fmaxf(m1, fmaxf(sc[u][2], sc[u][3]));
       }
       m = group4_max(fmaxf(m0, m1));
-      float l0 = 0.f, l1 = 0.f, l2 = 0.f, l3 = 0.f;
 #pragma unroll
       for (int u = 0; u < KT; ++u) {
         float e[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) e[i] = fast_exp2(sc[u][i] - m);
-        l0 += e[0];
-        l1 += e[1];
-        l2 += e[2];
-        l3 += e[3];
         C::set2(pf[u >> 1], 2 * (u & 1), e[0], e[1]);
         C::set2(pf[u >> 1], 2 * (u & 1) + 1, e[2], e[3]);
       }
@@ -313,19 +312,26 @@ __global__ void __launch_bounds__(kFpW * 64) fwd_plane_kernel(const FwdParams p)
         C::set2(pf[KS - 1], 2, 0.f, 0.f);
         C::set2(pf[KS - 1], 3, 0.f, 0.f);
       }
-      l = group4_sum((l0 + l1) + (l2 + l3));
     };
-    // four independent accumulators in turn (each accumulates every 4th product)
-    auto pv = [&](const Frag (&pf)[KS], f32x4 (&o)[4]) __attribute__((always_inline)) {
+    // five independent accumulators in turn (each accumulates every 5th
+    // product): O^T's four channel tiles and, from an all-ones A operand, the
+    // row sum l = sum_k P (the sum of the same rounded probabilities the O
+    // product weights V with, so O's weights sum to 1 exactly; every lane
+    // receives its query's sum)
+    auto pv = [&](const Frag (&pf)[KS], f32x4 (&o)[5]) __attribute__((always_inline)) {
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) o[dt] = C::mma(vt[dt][0], pf[0], f32x4{0.f, 0.f, 0.f, 0.f});
+      o[4] = C::mma(ones, pf[0], f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-      for (int j = 1; j < KS; ++j)
+      for (int j = 1; j < KS; ++j) {
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) o[dt] = C::mma(vt[dt][j], pf[j], o[dt]);
+        o[4] = C::mma(ones, pf[j], o[4]);
+      }
     };
     // O rows: lane (lr, lg) holds O[16t + lr][16dt + 4lg + i] (times l)
-    auto store_o = [&](int t, const f32x4 (&o)[4], float m, float l) __attribute__((always_inline)) {
+    auto store_o = [&](int t, const f32x4 (&o)[5], float m) __attribute__((always_inline)) {
+      const float l = o[4][0];
       const float inv = __builtin_amdgcn_rcpf(l);
       unsigned ov, os;
       tile_off(ooff, t, p.so[2], ov, os);
@@ -361,13 +367,15 @@ __global__ void __launch_bounds__(kFpW * 64) fwd_plane_kernel(const FwdParams p)
     // the O product of subtile t - 1 on the MFMA pipe while the VALU computes
     // the probabilities of subtile t; one MFMA is scheduled after every few
     // VALU instructions, so that neither waits for the other.
-    Frag qf[2];
-    f32x4 sc[KT], sn[KT], o[4];
+    // Q-hat of subtile t + 1 (qf[(t + 1) & 1]) feeds the logits of step t
+    // while that step's VALU already rotates subtile t + 2 into the other buffer
+    Frag qf[2][2];
+    f32x4 sc[KT], sn[KT], o[5];
     Frag pc[KS], pp[KS];
-    float mc = 0.f, lc = 1.f, mp = 0.f, lp = 1.f;
-    rot_q(qr[0], 0, qf);
-    logits(qf, sn);
-    rot_q(qr[1], 1, qf);
+    float mc = 0.f, mp = 0.f;
+    rot_q(qr[0], 0, qf[0]);
+    logits(qf[0], sn);
+    rot_q(qr[1], 1, qf[1]);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t <= KT; ++t) {
@@ -375,12 +383,13 @@ __global__ void __launch_bounds__(kFpW * 64) fwd_plane_kernel(const FwdParams p)
 #pragma unroll
         for (int u = 0; u < KT; ++u) sc[u] = sn[u];
       }
-      if (t + 1 < KT) logits(qf, sn);
+      if (t + 1 < KT) logits(qf[(t + 1) & 1], sn);
+      if (t + 2 < KT) rot_q(qr[t + 2], t + 2, qf[t & 1]);
       if (t >= 1) pv(pp, o);
-      if (t < KT) softmax(sc, pc, mc, lc);
-      const int nm = (t + 1 < KT ? 2 * KT : 0) + (t >= 1 ? 4 * KS : 0);
+      if (t < KT) softmax(sc, pc, mc);
+      const int nm = (t + 1 < KT ? 2 * KT : 0) + (t >= 1 ? 5 * KS : 0);
 #pragma unroll
-      for (int i = 0; i < 2 * KT + 4 * KS; ++i) {
+      for (int i = 0; i < 2 * KT + 5 * KS; ++i) {
         if (i < nm) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
           __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // four VALU
@@ -389,7 +398,6 @@ __global__ void __launch_bounds__(kFpW * 64) fwd_plane_kernel(const FwdParams p)
       __builtin_amdgcn_sched_barrier(0);
       // loads before stores: a later wait for one of these loads (the
       // vector memory counter is in order) then does not include the stores
-      if (t + 2 < KT) rot_q(qr[t + 2], t + 2, qf);   // (otherwise qf is no longer needed)
       if (t + kQpf < KT) load_q(rQ, t + kQpf, qr[t + kQpf]);
       if (t == KT - 2) load_k(rKn, kr);   // K-hat's last use (logits of subtile KT-1) is issued
       if (t == KT - 1) {
@@ -399,12 +407,11 @@ __global__ void __launch_bounds__(kFpW * 64) fwd_plane_kernel(const FwdParams p)
 #pragma unroll
       for (int i = kDmaPer * t; i < kDmaPer * (t + 1); ++i)
         if (i < kFpRows / 8) dma_row8(rVn, i);
-      if (t >= 1) store_o(t - 1, o, mp, lp);
+      if (t >= 1) store_o(t - 1, o, mp);
       if (t < KT) {
 #pragma unroll
         for (int j = 0; j < KS; ++j) pp[j] = pc[j];
         mp = mc;
-        lp = lc;
       }
       __builtin_amdgcn_sched_barrier(0);
     }
