@@ -485,9 +485,19 @@ bwd_plane_kernel(const BwdParams p) {
     // table rows shift .. N-1+shift of the packed table -> sTab (token order, swizzled)
     const int shift = 1 - p.has_cls;
     const f32x4* src = reinterpret_cast<const f32x4*>(p.rope) + shift * 16;
-    for (int i = tid; i < N * 16; i += kPlaneNW * 64) {
-      const int r = i >> 4, c = i & 15;
-      *reinterpret_cast<f32x4*>(&sTab[((r << 4) + (c ^ (r & 15))) * 4]) = src[i];
+    // all of a thread's loads first, then its LDS writes: one memory round
+    // trip instead of one per row group (N <= 256 rows: at most 8 per thread)
+    constexpr int TIT = kPlaneMaxN * 16 / (kPlaneNW * 64);
+    f32x4 tv[TIT];
+#pragma unroll
+    for (int j = 0; j < TIT; ++j) {
+      const int i = tid + j * kPlaneNW * 64;
+      tv[j] = i < N * 16 ? src[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int j = 0; j < TIT; ++j) {
+      const int i = tid + j * kPlaneNW * 64, r = i >> 4, c = i & 15;
+      if (i < N * 16) *reinterpret_cast<f32x4*>(&sTab[((r << 4) + (c ^ (r & 15))) * 4]) = tv[j];
     }
     // dS^T rows of waves with no key < N (keys >= round_up32(N)) enter the
     // dQ products but are never written by a sweep: zero them once, in both
