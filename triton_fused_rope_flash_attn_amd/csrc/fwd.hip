@@ -208,9 +208,7 @@ fwd_kernel(const FwdParams p) {
   // current pass of an item; the operand scales and the logit factor
   // 1 / (fq fk) of a rescaled pass (all 1 otherwise).
   float amax_q = 0.f, amax_k = 0.f;
-  typedef unsigned short vu16x2 __attribute__((ext_vector_type(2)));
-  vu16x2 amax_vb = {0, 0};   // FS: largest |V| bit patterns (16-bit I/O) of the pass, two lanes
-  float amax_vf = 0.f;       // FS: largest |V * fv| (32-bit I/O) of the pass
+  float amax_vf = 0.f;       // FS: largest |V * fv| of the pass
   float fq = 1.f, fk = 1.f, fsc = 1.f, fv = 1.f;
   float ifv = 1.f;   // 1 / fv of the item's kept pass (O comes out times fv)
   bool rescaled = false, redo = false;
@@ -247,6 +245,35 @@ fwd_kernel(const FwdParams p) {
                                     (unsigned)(kvb * (int)p.sk[2] * (int)ES));
           pv[it][x] = buf_load8<IO>(kr.v, (unsigned)((r * (int)p.sv[2] + 8 * cc) * (int)ES),
                                     (unsigned)(kvb * (int)p.sv[2] * (int)ES));
+        }
+      }
+      return;
+    }
+    if constexpr (VEC && !kTabLds && UNITS % NT == 0) {
+      // table rows from global memory too, through a descriptor over rows
+      // 0 .. N-1+shift: per-lane offsets fixed across chunks, the chunk's row
+      // in the uniform offset; rows >= N (zero K rows) read zeros
+      const int kvb = chunk_start(c);
+      const auto rT = make_rsrc(p.rope, (unsigned)((N + shift) * D * 4));
+#pragma unroll
+      for (int it = 0; it < ITER; ++it) {
+        const int u = tid + it * NT;
+        const int rp = u / CPR, cc = u - rp * CPR;
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+          const int r = 2 * rp + x;
+          pk[it][x] = buf_load8<IO>(kr.k, (unsigned)((r * (int)p.sk[2] + 8 * cc) * (int)ES),
+                                    (unsigned)(kvb * (int)p.sk[2] * (int)ES));
+          pv[it][x] = buf_load8<IO>(kr.v, (unsigned)((r * (int)p.sv[2] + 8 * cc) * (int)ES),
+                                    (unsigned)(kvb * (int)p.sv[2] * (int)ES));
+          const unsigned to = (unsigned)(((r + shift) * D + 8 * cc) * 4);
+          const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rT, to, (unsigned)(kvb * D * 4), 0);
+          const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(rT, to + 16, (unsigned)(kvb * D * 4), 0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            pcs[it][x][e] = __uint_as_float(a[e]);
+            pcs[it][x][4 + e] = __uint_as_float(b[e]);
+          }
         }
       }
       return;
@@ -339,24 +366,15 @@ fwd_kernel(const FwdParams p) {
             C::put8(&sK[slot][kperm(2 * rp + x) * LDK + 8 * cc], xk);
           }
           if constexpr (FS) {
-            // V in fp16, times fv (1 except in a rescaled pass); its range
-            // from the raw 16-bit patterns (|x| orders like its bits without
-            // the sign), two per packed integer max
+            // V in fp16, times fv (1 except in a rescaled pass, which alone
+            // multiplies); its range from the converted values
             float y[8];
             unpack8(pv[it][x], y);
+            if (rescaled) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) y[e] *= fv;
-            if constexpr (sizeof(IO) == 2) {
-              u32x4 w;
-              __builtin_memcpy(&w, &pv[it][x].v, 16);
-              vu16x2 m = __builtin_bit_cast(vu16x2, w[0] & 0x7fff7fffu);
-#pragma unroll
-              for (int k = 1; k < 4; ++k)
-                m = __builtin_elementwise_max(m, __builtin_bit_cast(vu16x2, w[k] & 0x7fff7fffu));
-              amax_vb = opaque_vec(__builtin_elementwise_max(amax_vb, m));
-            } else {
-              amax_vf = opaque(amax8(amax_vf, y));
+              for (int e = 0; e < 8; ++e) y[e] *= fv;
             }
+            amax_vf = opaque(amax8(amax_vf, y));
             *reinterpret_cast<f16x8*>(&sVt[slot][vrow(2 * rp + x) * LDK + 8 * cc]) = to_f16x8(y);
           } else if constexpr (TRV || VROW) {
             S* dst = &sVt[slot][vrow(2 * rp + x) * LDK + 8 * cc];
@@ -833,23 +851,26 @@ fwd_kernel(const FwdParams p) {
   // before the softmax of block j, so that those MFMAs run while the VALU
   // computes block j's probabilities; two blocks per trip alternate the two
   // logit accumulators without copies.
-  auto chunk_serial = [&](const S* __restrict__ cK, const VS* __restrict__ cV, int kvb) __attribute__((always_inline)) {
+  // MASKC: the chunk may hold keys >= N (an item's first chunk, the ragged
+  // one); the other chunks of an item are full.
+  auto chunk_serial = [&](auto maskc, const S* __restrict__ cK, const VS* __restrict__ cV, int kvb) __attribute__((always_inline)) {
     const int nkeys = min(KC, N - kvb);
     if constexpr (sizeof(S) == 2 && (QT == 1 || (VEC && D >= 128))) {
-      // every block goes through the masked softmax (a key limit past the
-      // block for full ones): one inlined copy per call site keeps the
-      // pipelined loop within the register budget
+      // every block of a chunk goes through the same softmax (with MASKC the
+      // masked one, with a key limit past the block for full ones): one
+      // inlined copy per call site keeps the pipelined loop within the
+      // register budget
       const int nb = (nkeys + 31) >> 5;
       SAcc sA, sB;
       blk_logits(cK, 0, sA);
       int j = 0;
       for (; j + 1 < nb; j += 2) {
         blk_logits(cK, j + 1, sB);
-        blk_out(std::true_type{}, cV, kvb, j, sA);
+        blk_out(maskc, cV, kvb, j, sA);
         if (j + 2 < nb) blk_logits(cK, j + 2, sA);
-        blk_out(std::true_type{}, cV, kvb, j + 1, sB);
+        blk_out(maskc, cV, kvb, j + 1, sB);
       }
-      if (j < nb) blk_out(std::true_type{}, cV, kvb, j, sA);   // odd block count: last logits in sA
+      if (j < nb) blk_out(maskc, cV, kvb, j, sA);   // odd block count: last logits in sA
     } else {
       // two subtiles per wave at D <= 64 or with element-wise access, or fp32
       // compute (split operands): two blocks' logits do not fit beside their
@@ -994,13 +1015,7 @@ fwd_kernel(const FwdParams p) {
         // once more.
         if (c == nch - 1) {
           {
-            // |V| of the raw 16-bit patterns as fp32 (bf16: the top half of an
-            // fp32; fp16: converted) for the wave maximum
-            const unsigned short vb = max(amax_vb[0], amax_vb[1]);
-            float va = amax_vf;
-            if constexpr (std::is_same<IO, bf16>::value) va = __uint_as_float((unsigned)vb << 16) * fv;
-            if constexpr (std::is_same<IO, f16>::value) va = (float)__builtin_bit_cast(f16, vb) * fv;
-            const unsigned rq = wave_max_bits(amax_q), rk = wave_max_bits(amax_k), rv = wave_max_bits(va);
+            const unsigned rq = wave_max_bits(amax_q), rk = wave_max_bits(amax_k), rv = wave_max_bits(amax_vf);
             if (lane == 0) sRange[wave] = u32x4{rq, rk, rv, 0u};
           }
           lds_barrier();
@@ -1047,7 +1062,8 @@ fwd_kernel(const FwdParams p) {
       } else {
         mem();
         lds_barrier();
-        if (nt > 0) chunk_serial(sK[slot], sVt[slot], chunk_start(c));
+        // (chunk 0 starts at the last chunk's keys: only it can hold keys >= N)
+        if (nt > 0) chunk_serial(firstc, sK[slot], sVt[slot], chunk_start(c));
         if constexpr (XR) {
           if (xi) xrow_chunk(sK[slot], sVt[slot], chunk_start(c), c == 0);
         }
@@ -1061,7 +1077,6 @@ fwd_kernel(const FwdParams p) {
       // a rescaled second pass (its first chunk is already on the way; no
       // Q prefetch or deferred store exists with these operands); no store
       amax_q = amax_k = amax_vf = 0.f;
-      amax_vb = vu16x2{0, 0};
       if constexpr (XR) ++npass;
       if (redo) {
         redo = false;
