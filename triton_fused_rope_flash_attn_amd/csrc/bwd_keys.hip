@@ -268,6 +268,20 @@ __global__ void __launch_bounds__(512) bwd_keys_kernel(const BwdParams p) {
   // have zero K-hat / V rows: their P is clamped to [0, 1], dS = -P delta is
   // finite and only reaches dK / dV rows that are never stored.
   auto pdk = [&](int j, const f32x4 (&sacc)[2], const f32x4 (&pacc)[2]) __attribute__((always_inline)) {
+    // the transposed operands of the first PF channel tiles are read before
+    // the probabilities are formed, and each product then reads the tile PF
+    // further on: every product waits for a read issued PF products earlier
+    constexpr int PF = 3;
+    Frag ag[DT];
+    HFrag aq[DT];
+    auto rd = [&](int d) __attribute__((always_inline)) {
+      const int o0 = (32 * j + qt0) * LDQ + 16 * d + 4 * (lr & 3);
+      const int o1 = (32 * j + qt1) * LDQ + 16 * d + 4 * (lr & 3);
+      ag[d] = C::tr(&sG[o0], &sG[o1]);
+      aq[d] = H::tr(&sQf[o0], &sQf[o1]);
+    };
+#pragma unroll
+    for (int d = 0; d < PF; ++d) rd(d);
     float pv[8], dsv[8];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -283,12 +297,9 @@ __global__ void __launch_bounds__(512) bwd_keys_kernel(const BwdParams p) {
 #pragma unroll
     for (int d = 0; d < DT; ++d) {
       // A = dO^T / Q-hat^T rows 16d.., k-slot e <-> query 32j + 8lg + e (the P / dS order)
-      const int o0 = (32 * j + qt0) * LDQ + 16 * d + 4 * (lr & 3);
-      const int o1 = (32 * j + qt1) * LDQ + 16 * d + 4 * (lr & 3);
-      const Frag ag = C::tr(&sG[o0], &sG[o1]);
-      const HFrag aq = H::tr(&sQf[o0], &sQf[o1]);
-      dvacc[d] = C::mma(ag, pf, dvacc[d]);
-      dkacc[d] = H::mma(aq, dsf, dkacc[d]);
+      if (d + PF < DT) rd(d + PF);
+      dvacc[d] = C::mma(ag[d], pf, dvacc[d]);
+      dkacc[d] = H::mma(aq[d], dsf, dkacc[d]);
     }
   };
   prefetch(0);
@@ -307,7 +318,18 @@ __global__ void __launch_bounds__(512) bwd_keys_kernel(const BwdParams p) {
       sp(j, sA, pA);
       sp(min(j + 1, nbj - 1), sB, pB);
       pdk(j, sA, pA);
-      if (j + 1 < nbj) pdk(j + 1, sB, pB);
+      if (j + 1 < nbj) {
+        pdk(j + 1, sB, pB);
+        // the last block's order, which the scheduler otherwise collapses to
+        // one read ahead: the 12 reads of its first three channel tiles, then
+        // per tile its two products and the 4 reads three tiles on
+        __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+#pragma unroll
+        for (int d = 0; d < DT; ++d) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+          if (d + 3 < DT) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        }
+      }
     }
   }
 
