@@ -12,7 +12,8 @@
 // workgroup per (plane, 128-key tile), the layout of the generic dK/dV kernel
 // (bwd.hip): each wave's K-hat and V rows are MFMA B operands in registers,
 // and the Q-hat / dO rows of each 64-query stage are staged in LDS (rows
-// vperm'd) and read transposed for the dV / dK products.
+// vperm'd, two buffers: the next stage is committed between the current
+// stage's two query blocks) and read transposed for the dV / dK products.
 //
 // Products in fp16.  The logits take fp16 Q-hat * c2 * fq and K-hat * fk as
 // in the forward pass; dK-hat takes dS in fp16, scaled by a power of two sig,
@@ -64,10 +65,13 @@ __global__ void __launch_bounds__(512) bwd_keys_kernel(const BwdParams p) {
   constexpr unsigned ES = sizeof(IO);
   static_assert(KROWS == kKeysRows && sizeof(IO) == 2 && ITER * NT == QS * CPR, "tile shape");
 
-  __shared__ __attribute__((aligned(16))) f16 sQf[QS * LDQ];       // fp16 Q-hat * c2 * fq (rows vperm'd)
-  __shared__ __attribute__((aligned(16))) bf16 sG[QS * LDQ];       // dO rows (vperm'd)
-  __shared__ __attribute__((aligned(16))) float sL2[QS];           // -LSE2 * fq * fk
-  __shared__ __attribute__((aligned(16))) float sDl[QS];           // -delta * sig
+  // stage buffers (two: the next stage is committed during the current one,
+  // into the buffer the previous stage read, which every wave finished before
+  // the current stage's barrier; one barrier per stage)
+  __shared__ __attribute__((aligned(16))) f16 sQf[2][QS * LDQ];    // fp16 Q-hat * c2 * fq (rows vperm'd)
+  __shared__ __attribute__((aligned(16))) bf16 sG[2][QS * LDQ];    // dO rows (vperm'd)
+  __shared__ __attribute__((aligned(16))) float sL2[2][QS];        // -LSE2 * fq * fk
+  __shared__ __attribute__((aligned(16))) float sDl[2][QS];        // -delta * sig
   __shared__ float sRed[NW][6];
 
   const int N = p.N;
@@ -206,14 +210,14 @@ __global__ void __launch_bounds__(512) bwd_keys_kernel(const BwdParams p) {
     }
   };
   const float l2seed = kLog2e * fq * fk;
-  auto commit = [&](int qb) __attribute__((always_inline)) {
+  auto commit = [&](int b, int qb) __attribute__((always_inline)) {
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
       const int c = tid + it * NT;
       const int r = c / CPR, cc = c - r * CPR;
       const int off = vperm(r) * LDQ + 8 * cc;
       if (!raw) {
-        *reinterpret_cast<f16x8*>(&sQf[off]) = pqf[it].v;
+        *reinterpret_cast<f16x8*>(&sQf[b][off]) = pqf[it].v;
       } else {
         // rescaled operands: rotate the row here (rows >= N are zero)
         const int gr = qb + r;
@@ -229,45 +233,45 @@ __global__ void __launch_bounds__(512) bwd_keys_kernel(const BwdParams p) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) xq[e] = 0.f;
         }
-        *reinterpret_cast<f16x8*>(&sQf[off]) = to_f16x8(xq);
+        *reinterpret_cast<f16x8*>(&sQf[b][off]) = to_f16x8(xq);
       }
       if constexpr (std::is_same<IO, bf16>::value) {
-        *reinterpret_cast<typename Raw8<IO>::vec*>(&sG[off]) = pg[it].v;
+        *reinterpret_cast<typename Raw8<IO>::vec*>(&sG[b][off]) = pg[it].v;
       } else {
         float xg[8];
         unpack8(pg[it], xg);
-        C::put8(&sG[off], xg);
+        C::put8(&sG[b][off], xg);
       }
     }
     if (tid < QS) {   // negated: they seed the S and dP accumulators
-      sL2[tid] = qb + tid < N ? -pl * l2seed : -INFINITY;
-      sDl[tid] = qb + tid < N ? -pd * sig : 0.f;
+      sL2[b][tid] = qb + tid < N ? -pl * l2seed : -INFINITY;
+      sDl[b][tid] = qb + tid < N ? -pd * sig : 0.f;
     }
   };
 
   // S and dP of query block j (32 queries) of the stage for the wave's keys;
   // query 32j + 8lg + 4h + i of accumulator h, element i (see the A rows).
-  auto sp = [&](int j, f32x4 (&sacc)[2], f32x4 (&pacc)[2]) __attribute__((always_inline)) {
-    sacc[0] = *reinterpret_cast<const f32x4*>(&sL2[32 * j + 8 * lg]);
-    sacc[1] = *reinterpret_cast<const f32x4*>(&sL2[32 * j + 8 * lg + 4]);
-    pacc[0] = *reinterpret_cast<const f32x4*>(&sDl[32 * j + 8 * lg]);
-    pacc[1] = *reinterpret_cast<const f32x4*>(&sDl[32 * j + 8 * lg + 4]);
+  auto sp = [&](int b, int j, f32x4 (&sacc)[2], f32x4 (&pacc)[2]) __attribute__((always_inline)) {
+    sacc[0] = *reinterpret_cast<const f32x4*>(&sL2[b][32 * j + 8 * lg]);
+    sacc[1] = *reinterpret_cast<const f32x4*>(&sL2[b][32 * j + 8 * lg + 4]);
+    pacc[0] = *reinterpret_cast<const f32x4*>(&sDl[b][32 * j + 8 * lg]);
+    pacc[1] = *reinterpret_cast<const f32x4*>(&sDl[b][32 * j + 8 * lg + 4]);
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int ql = 32 * j + vperm(8 * (lr >> 2) + 4 * h + (lr & 3));
-        const HFrag a = H::lds(&sQf[ql * LDQ + 32 * s + 8 * lg]);
-        const Frag b = C::lds(&sG[ql * LDQ + 32 * s + 8 * lg]);
+        const HFrag a = H::lds(&sQf[b][ql * LDQ + 32 * s + 8 * lg]);
+        const Frag g = C::lds(&sG[b][ql * LDQ + 32 * s + 8 * lg]);
         sacc[h] = H::mma(a, kf[s], sacc[h]);
-        pacc[h] = C::mma(b, vf[s], pacc[h]);
+        pacc[h] = C::mma(g, vf[s], pacc[h]);
       }
     }
   };
   // P and dS of block j, dV += P^T dO, dK-hat += (sig dS)^T Q-hat.  Keys >= N
   // have zero K-hat / V rows: their P is clamped to [0, 1], dS = -P delta is
   // finite and only reaches dK / dV rows that are never stored.
-  auto pdk = [&](int j, const f32x4 (&sacc)[2], const f32x4 (&pacc)[2]) __attribute__((always_inline)) {
+  auto pdk = [&](int b, int j, const f32x4 (&sacc)[2], const f32x4 (&pacc)[2]) __attribute__((always_inline)) {
     // the transposed operands of the first PF channel tiles are read before
     // the probabilities are formed, and each product then reads the tile PF
     // further on: every product waits for a read issued PF products earlier
@@ -277,8 +281,8 @@ __global__ void __launch_bounds__(512) bwd_keys_kernel(const BwdParams p) {
     auto rd = [&](int d) __attribute__((always_inline)) {
       const int o0 = (32 * j + qt0) * LDQ + 16 * d + 4 * (lr & 3);
       const int o1 = (32 * j + qt1) * LDQ + 16 * d + 4 * (lr & 3);
-      ag[d] = C::tr(&sG[o0], &sG[o1]);
-      aq[d] = H::tr(&sQf[o0], &sQf[o1]);
+      ag[d] = C::tr(&sG[b][o0], &sG[b][o1]);
+      aq[d] = H::tr(&sQf[b][o0], &sQf[b][o1]);
     };
 #pragma unroll
     for (int d = 0; d < PF; ++d) rd(d);
@@ -303,23 +307,30 @@ __global__ void __launch_bounds__(512) bwd_keys_kernel(const BwdParams p) {
     }
   };
   prefetch(0);
-  for (int qb = 0; qb < N; qb += QS) {
+  // One 64-query stage in buffer B (a compile-time constant: two stages per
+  // trip, so the buffer addresses fold into the LDS instructions' offsets).
+  auto stage = [&](int qb, auto bufc) __attribute__((always_inline)) {
+    constexpr int B = decltype(bufc)::value;
     const int rows = min(QS, round_up32(N - qb));
-    lds_barrier();
-    commit(qb);
-    lds_barrier();
-    prefetch(qb + QS);   // past the last stage: rows >= N, read as 0
+    lds_barrier();   // this stage's commit (made during the previous stage) is visible
     // Two query blocks per trip: the S / dP products of block j+1 go to the
     // MFMA pipe before block j's probabilities are computed on the VALU (a
     // ragged last stage recomputes block j instead and skips its update).
     const int nbj = rows / 32;
     for (int j = 0; j < nbj; j += 2) {
       f32x4 sA[2], pA[2], sB[2], pB[2];
-      sp(j, sA, pA);
-      sp(min(j + 1, nbj - 1), sB, pB);
-      pdk(j, sA, pA);
+      sp(B, j, sA, pA);
+      sp(B, min(j + 1, nbj - 1), sB, pB);
+      pdk(B, j, sA, pA);
+      // the next stage goes into the other buffer (last read in the previous
+      // stage, which every wave finished before this stage's barrier), and
+      // the stage after it is prefetched (past the last stage: rows >= N)
+      if (qb + QS < N) {
+        commit(B ^ 1, qb + QS);
+        prefetch(qb + 2 * QS);
+      }
       if (j + 1 < nbj) {
-        pdk(j + 1, sB, pB);
+        pdk(B, j + 1, sB, pB);
         // the last block's order, which the scheduler otherwise collapses to
         // one read ahead: the 12 reads of its first three channel tiles, then
         // per tile its two products and the 4 reads three tiles on
@@ -331,6 +342,16 @@ __global__ void __launch_bounds__(512) bwd_keys_kernel(const BwdParams p) {
         }
       }
     }
+  };
+  {
+    commit(0, 0);
+    prefetch(QS);
+    int qb = 0;
+    for (; qb + QS < N; qb += 2 * QS) {
+      stage(qb, std::integral_constant<int, 0>{});
+      stage(qb + QS, std::integral_constant<int, 1>{});
+    }
+    if (qb < N) stage(qb, std::integral_constant<int, 0>{});
   }
 
   // ---- epilogue: lane holds dV / dK-hat of key kv_first + lr, channels 16d + 4lg + (0..3) ----
