@@ -437,7 +437,8 @@ def main():
     bwd_cfg = _lib.tile_config(desc, 1)
     fwd_cfg = _lib.tile_config(desc, 0)
     bwd_kernel = {0: "bwd_plane_kernel", 1: "bwd_dq_kernel + bwd_dkdv_kernel",
-                  2: "bwd_dq_kernel + bwd_keys_kernel"}[bwd_cfg[0]]
+                  2: "bwd_dq_kernel + bwd_keys_kernel",
+                  3: "bwd_ds_prep_kernel + bwd_keys_kernel + bwd_ds_dq_kernel"}[bwd_cfg[0]]
 
     traffic = None
     if os.path.exists(TRAFFIC_FILE):

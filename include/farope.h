@@ -120,8 +120,15 @@ size_t farope_attn_residual_elems(const farope_attn_desc* desc);
  * rotating Q again for every key tile; then, of those shapes at head_dim
  * 128, 2 * batch * heads * seq_len fp32 values (from a 256-byte boundary):
  * each query row's {|dO|_2, max |Q-hat * scale * log2(e)|}, from which the
- * key-tile kernel fixes its fp16 operand scalings.  0 on an invalid
- * descriptor.
+ * key-tile kernel fixes its fp16 operand scalings.  At the stored-dS shapes
+ * (16-bit I/O, bf16 compute, head_dim 128, at most one key past the 128-key
+ * tiles) the larger of that and the stored-dS layout, whose parts each start
+ * on a 256-byte boundary: the delta rows; with a lone last key one partial
+ * dK / dV row pair per 64-row tile; the fp16 rotated Q rows; the row
+ * statistics; with a lone last key its dS per query row; one int32 exponent
+ * per key tile; the key tiles' fp16 K-hat rows; and their fp16 dS^T rows
+ * (pitch seq_len rounded up to 64), which the dQ GEMM reads instead of
+ * recomputing the logits.  0 on an invalid descriptor.
  */
 size_t farope_attn_bwd_workspace_elems(const farope_attn_desc* desc);
 
@@ -172,7 +179,9 @@ int farope_attn_bwd_dq(const farope_attn_desc* desc,
 /*
  * Whole backward pass (what TritonAttention.backward does, FA:1067-1138):
  * picks the fused one-launch kernel when the plane fits on chip (D = 64,
- * N <= 256), else dq (which also writes delta) followed by dk/dv.
+ * N <= 256); at the stored-dS shapes with vector access to every tensor a
+ * row pass (delta), key tiles that keep dS, and dQ as one GEMM over it;
+ * else dq (which also writes delta) followed by dk/dv.
  * delta_ws: caller-owned fp32 workspace of
  * farope_attn_bwd_workspace_elems(desc) elements.
  * o_res: NULL, or the residual buffer the forward filled.
@@ -197,10 +206,11 @@ int farope_attn_bwd(const farope_attn_desc* desc,
  * lives in a static device array of FAROPE_NOALLOC_MAX_ROWS fp32 values that
  * the library holds on every device it runs on until the process ends; calls
  * that need more return FAROPE_ERR_SCRATCH before anything is launched.  The
- * rotated Q rows and row statistics of farope_attn_bwd_workspace_elems go
- * there too when the whole workspace fits, and the kernels are then those of
- * farope_attn_bwd; otherwise the generic dK/dV kernel runs and rotates Q
- * itself (results within rounding of farope_attn_bwd's).  The one-pass
+ * rest of farope_attn_bwd_workspace_elems (rotated Q rows, row statistics,
+ * the stored-dS planes) goes there too when the whole workspace fits, and the
+ * kernels are then those of farope_attn_bwd; otherwise the split path's
+ * kernels run, the generic dK/dV kernel rotating Q itself (results within
+ * rounding of farope_attn_bwd's).  The one-pass
  * backward uses no workspace and takes any size.  Allocates nothing.  Calls
  * on one device share that array, so calls that overlap on one device
  * (concurrent streams or threads) race; calls ordered on one stream do not.
@@ -223,7 +233,8 @@ int farope_attn_bwd_noalloc(const farope_attn_desc* desc,
  * 1 = backward.  out[0] = variant (fwd: 0 = persistent pipelined kernel,
  * 1 = one wave per (b, h) plane for 193 <= N <= 208 at head_dim 64 with
  * 16-bit tensors, assuming vector access; bwd: 0 fused, 1 split, 2 split with
- * the key-tile kernel), out[1] = query (fwd) or key (bwd) rows per work item,
+ * the key-tile kernel, 3 key tiles that store dS and dQ as one GEMM over it,
+ * assuming vector access), out[1] = query (fwd) or key (bwd) rows per work item,
  * out[2] = work items per (b, h) plane, out[3] = threads per workgroup.  When 1 to 8 rows are left past out[1] * out[2] (N = 1025 with
  * 128- or 256-row items), they are computed by the tail-row kernels (or, for
  * a single row with fp16 logit operands, by one designated item of each plane

@@ -66,8 +66,9 @@ def test_rope_packed_elems(lib):
 @pytest.mark.parametrize(
     "N,D,has_cls,fwd_var,fwd_items,bwd_var",
     [(197, 64, 1, 1, 1, 0), (208, 64, 0, 1, 1, 0), (192, 64, 1, 0, 1, 0), (256, 64, 0, 0, 1, 0),
-     (257, 64, 1, 0, 1, 1), (1025, 128, 1, 0, 4, 2), (197, 128, 1, 0, 1, 2),
-     (197, 256, 1, 0, 3, 1), (257, 256, 1, 0, 4, 1), (1100, 128, 1, 0, 5, 2)],
+     (257, 64, 1, 0, 1, 1), (1025, 128, 1, 0, 4, 3), (197, 128, 1, 0, 1, 3),
+     (197, 256, 1, 0, 3, 1), (257, 256, 1, 0, 4, 1), (1100, 128, 1, 0, 5, 3),
+     (3970, 128, 1, 0, 16, 2)],
 )
 def test_tile_table(lib, N, D, has_cls, fwd_var, fwd_items, bwd_var):
     """Forward variant 1 (one wave per plane) covers planes of 193 .. 208 tokens at D = 64."""
@@ -80,6 +81,35 @@ def test_tile_table(lib, N, D, has_cls, fwd_var, fwd_items, bwd_var):
         assert left <= 8 and t[2] >= 1
         assert left > 0 or (t[2] - 1) * t[1] < N   # otherwise: no empty block
     assert f[3] % 64 == 0 and b[3] % 64 == 0
+
+
+def _ds_elems(B, H, N, D):
+    """Workspace of the stored-dS backward (None where it does not apply: more
+    than one key past the 128-key tiles), in fp32 elements, each part from a
+    64-float boundary: delta rows; with a lone last key one partial dK / dV
+    row pair per 64-row tile; fp16 Q-hat rows; {|dO|, max |Q-hat|} per row;
+    with a lone last key its dS per row; an int32 exponent per key tile; fp16
+    K-hat rows of the key tiles; fp16 dS^T rows of the key tiles (pitch N
+    rounded up to 64)."""
+    r = N % 128
+    t = r if N >= 128 and 0 < r <= 8 else 0
+    if t > 1:
+        return None
+    planes, rows = B * H, B * H * N
+    n_kt = N // 128 if t else -(-N // 128)
+    kp, n_pt, nqp = n_kt * 128, -(-N // 64), (N + 63) // 64 * 64
+
+    def al(x):
+        return (x + 63) // 64 * 64
+
+    xk = al(rows)
+    hat = al(xk + (planes * n_pt * 2 * D if t else 0))
+    stat = al(hat + rows * D // 2)
+    dsl = al(stat + 2 * rows)
+    kexp = al(dsl + (rows if t else 0))
+    khat = al(kexp + planes * n_kt)
+    dst = al(khat + planes * kp * D // 2)
+    return dst + planes * kp * nqp // 2
 
 
 @pytest.mark.parametrize(
@@ -115,8 +145,13 @@ def test_bwd_workspace_elems(lib, B, H, N, D, io, ct, extra, hat):
     if hat:
         n = (n + 63) // 64 * 64 + B * H * N * D // 2
     if hat and D == 128:
-        assert _lib.tile_config(desc, 1)[0] == 2
         n = (n + 63) // 64 * 64 + 2 * B * H * N
+        ds = _ds_elems(B, H, N, D)
+        if ds is not None:   # the stored-dS backward: the larger of the two layouts
+            assert _lib.tile_config(desc, 1)[0] == 3
+            n = max(n, ds)
+        else:
+            assert _lib.tile_config(desc, 1)[0] == 2
     assert _lib.bwd_workspace_elems(desc) == n
     bad = _lib.make_desc(B, H, N, 60, N - 1, True, io, ct, 0.125)
     assert _lib.bwd_workspace_elems(bad) == 0

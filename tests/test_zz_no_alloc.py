@@ -1,11 +1,11 @@
 """farope_attn_bwd_noalloc (static device workspace, no allocation) against
 farope_attn_bwd (caller workspace), both called through the C ABI.
 
-Split-path calls in a row (N = 257 at D = 128 with the last row and key
-folded into the dQ tiles, N = 257 at D = 64, then a smaller D = 128 problem)
-and one one-pass call: the same kernels run with the delta rows in the library's
-static array instead of a caller buffer, so dQ, dK and dV must be identical
-bit for bit.  The second call reuses the array the first one left behind.
+Workspace-path calls in a row (N = 257 at D = 128 through the stored-dS
+backward, N = 257 at D = 64 through the split path, then a smaller D = 128
+problem) and one one-pass call: the same kernels run with their workspace in
+the library's static array instead of a caller buffer, so dQ, dK and dV must
+be identical bit for bit.  The second call reuses the array the first one left behind.
 The one-pass backward uses no workspace at all, so the no-alloc entry also
 takes a one-pass call larger than the static array (4.26 Mi rows).
 """
@@ -78,10 +78,10 @@ def test_noalloc_one_pass_beyond_static_rows():
 
 
 def test_noalloc_matches_workspace_entry_two_calls():
-    # N = 257, D = 128: the last row and key ride along the dQ tiles (their
-    # partial dK / dV rows go to the workspace past the delta rows); dK / dV
-    # from the key tiles with fp16 dS products (variant 2)
-    assert _one(2, 3, 16, True, 128, seed=24) == 2
+    # N = 257, D = 128: the stored-dS backward (variant 3: row pass, key tiles
+    # that keep dS, dQ GEMM; the last key's partial dK / dV rows and dS, the
+    # dS^T and K-hat planes all in the static array)
+    assert _one(2, 3, 16, True, 128, seed=24) == 3
     assert _one(4, 6, 16, True, 64, seed=21) == 1    # split path, N = 257
-    assert _one(2, 3, 7, True, 128, seed=22) == 2    # smaller, split path (D = 128)
+    assert _one(2, 3, 7, True, 128, seed=22) == 3    # smaller, stored-dS path (one ragged key tile)
     assert _one(2, 4, 14, True, 64, seed=23) == 0    # one-pass path (no workspace used)

@@ -20,7 +20,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 INCLUDE = os.path.join(REPO_DIR, "include")
 LIB_NAME = "libfarope.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["api.hip", "fwd.hip", "fwd_plane.hip", "bwd.hip", "bwd_fused.hip", "bwd_keys.hip", "tail.hip"]
+SOURCES = ["api.hip", "fwd.hip", "fwd_plane.hip", "bwd.hip", "bwd_fused.hip", "bwd_keys.hip", "bwd_ds.hip", "tail.hip"]
 # Per-file code generation options.  fwd_plane.hip keeps its MFMA results in
 # VGPRs (they feed the softmax VALU directly) and its resident operand
 # fragments in AGPRs.

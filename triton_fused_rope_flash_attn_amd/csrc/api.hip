@@ -259,12 +259,86 @@ int64_t bwd_ws_elems(const farope_attn_desc* d) { return bwd_ws(d, false).total;
 bool keys_possible(const farope_attn_desc* d) {
   return qhat_possible(d) && d->head_dim == kKeysRows && d->compute_dtype == FAROPE_BF16;
 }
-// Caller workspace of farope_attn_bwd: bwd_ws, then (keys_possible, from a
+// Caller workspace of the split path with key tiles: bwd_ws, then (from a
 // 256-byte boundary) one {|dO|_2, max |Q-hat c2|} pair per query row.
 int64_t stat_offset(const farope_attn_desc* d) { return (bwd_ws(d, true).total + 63) & ~int64_t(63); }
-int64_t bwd_caller_ws(const farope_attn_desc* d) {
+int64_t split_caller_ws(const farope_attn_desc* d) {
   if (!keys_possible(d)) return bwd_ws(d, true).total;
   return stat_offset(d) + 2 * (int64_t)d->batch * d->heads * d->seq_len;
+}
+
+// The stored-dS backward (bwd_ds.hip): the key tiles' shapes (16-bit I/O, bf16
+// compute, head_dim 128) with at most one key past the full key tiles, and a
+// dS^T plane that 32-bit offsets address.  (Vector access to every tensor is
+// checked at the call.)
+constexpr int kDsD = 128;
+int ds_pitch(int N) { return (N + 63) & ~63; }   // 128-byte rows
+bool ds_possible(const farope_attn_desc* d) {
+  if (bwd_fused(d) || d->io_dtype == FAROPE_F32 || d->compute_dtype != FAROPE_BF16 || d->head_dim != kDsD)
+    return false;
+  const int planes = d->batch * d->heads, N = d->seq_len;
+  if (tail_of(planes, N, kKeysRows) > 1) return false;
+  const int64_t n_kt = main_blocks(planes, N, kKeysRows), kp = n_kt * kKeysRows;
+  return n_kt <= kDsMaxKeyTiles && kp * ds_pitch(N) * 2 < ((int64_t)1 << 31);
+}
+// Its workspace, in fp32 elements, each part from a 256-byte boundary: delta
+// rows; (lone last key) one partial dK-hat / dV row pair per row-pass tile;
+// fp16 Q-hat * c2 rows; row statistics; (lone last key) its dS per row; the
+// key tiles' exponents (int32); their fp16 K-hat * fk rows; their fp16
+// sig dS^T rows.
+struct DsWs {
+  int64_t xk, hat, stat, dsl, kexp, khat, dst, total;
+};
+DsWs ds_ws(const farope_attn_desc* d) {
+  const int planes = d->batch * d->heads, N = d->seq_len;
+  const int64_t rows = (int64_t)planes * N;
+  const bool last = tail_of(planes, N, kKeysRows) == 1;
+  const int64_t n_kt = main_blocks(planes, N, kKeysRows), kp = n_kt * kKeysRows;
+  const int64_t n_pt = cdiv(N, kDsPrepRows);
+  auto al = [](int64_t x) { return (x + 63) & ~int64_t(63); };
+  DsWs w{};
+  w.xk = al(rows);
+  w.hat = al(w.xk + (last ? planes * n_pt * 2 * kDsD : 0));
+  w.stat = al(w.hat + rows * kDsD / 2);
+  w.dsl = al(w.stat + 2 * rows);
+  w.kexp = al(w.dsl + (last ? rows : 0));
+  w.khat = al(w.kexp + planes * n_kt);
+  w.dst = al(w.khat + planes * kp * kDsD / 2);
+  w.total = w.dst + planes * kp * ds_pitch(N) / 2;
+  return w;
+}
+
+// Caller workspace of farope_attn_bwd: enough for whichever path the call
+// takes.
+int64_t bwd_caller_ws(const farope_attn_desc* d) {
+  const int64_t s = split_caller_ws(d);
+  if (!ds_possible(d)) return s;
+  const int64_t t = ds_ws(d).total;
+  return t > s ? t : s;
+}
+
+// Stored-dS backward: row pass, key tiles (storing dS), dQ GEMM, and the
+// merge of the lone last key's partial rows.
+int ds_pass(BwdParams p, const farope_attn_desc* d, float* ws, hipStream_t st) {
+  const DsWs w = ds_ws(d);
+  const int planes = p.B * p.H, N = p.N;
+  const bool last = tail_of(planes, N, kKeysRows) == 1;
+  p.qhat_f = ws + w.hat;
+  p.row_stat = ws + w.stat;
+  p.xk_ws = last ? ws + w.xk : nullptr;
+  p.dslast = last ? ws + w.dsl : nullptr;
+  p.kexp = reinterpret_cast<int*>(ws + w.kexp);
+  p.khat = ws + w.khat;
+  p.ds_t = ws + w.dst;
+  p.nqp = ds_pitch(N);
+  p.n_kt = main_blocks(planes, N, kKeysRows);
+  FAROPE_TRY(launch_rc(launch_bwd_ds_prep(p, d->io_dtype, st)));
+  p.n_blk = p.n_kt;
+  FAROPE_TRY(launch_rc(launch_bwd_keys(p, d->io_dtype, st)));
+  FAROPE_TRY(launch_rc(launch_bwd_ds_dq(p, d->io_dtype, st)));
+  if (last)
+    FAROPE_TRY(launch_rc(launch_bwd_tail_key_merge(p, d->io_dtype, kDsD, cdiv(N, kDsPrepRows), st)));
+  return FAROPE_OK;
 }
 
 int bwd_impl(const farope_attn_desc* desc, const void* q, const int64_t q_stride[4],
@@ -322,6 +396,11 @@ int bwd_impl(const farope_attn_desc* desc, const void* q, const int64_t q_stride
     p.n_blk = 1;
     return launch_rc(launch_bwd_fused(p, desc->io_dtype, desc->compute_dtype, st));
   }
+  // the stored-dS backward (the static workspace only when all of it fits)
+  if (ds_possible(desc) && p.vec_q && p.vec_k && p.vec_v && p.vec_o && p.vec_do && p.vec_dq &&
+      p.vec_dk && p.vec_dv && reinterpret_cast<uintptr_t>(delta_ws) % 16 == 0 &&
+      (!static_ws || ds_ws(desc).total <= kScratchFloats))
+    return ds_pass(p, desc, delta_ws, st);
   // dQ (and delta, which the dK/dV pass reads for every row) before dK / dV
   if (key_from_dq(desc, p.vec_k && p.vec_v))
     p.xk_ws = delta_ws + (int64_t)desc->batch * desc->heads * desc->seq_len;
@@ -340,7 +419,7 @@ int bwd_impl(const farope_attn_desc* desc, const void* q, const int64_t q_stride
   // the key tiles with fp16 dS products take the dK/dV pass (the static
   // workspace only when all of it fits)
   if (p.qhat_f && keys_possible(desc) && p.vec_k && p.vec_v && p.vec_o && p.vec_dq && p.vec_dk &&
-      p.vec_dv && (!static_ws || bwd_caller_ws(desc) <= kScratchFloats))
+      p.vec_dv && (!static_ws || split_caller_ws(desc) <= kScratchFloats))
     p.row_stat = delta_ws + stat_offset(desc);
   FAROPE_TRY(dq_pass(p, desc, true, st));
   return dkdv_pass(p, desc, st);
@@ -407,7 +486,7 @@ int farope_tile_config(const farope_attn_desc* desc, int32_t which, int32_t out[
     out[3] = fwd_threads(D);
   } else {
     const bool fu = bwd_fused(desc);
-    out[0] = fu ? BWD_FUSED : keys_possible(desc) ? BWD_SPLIT16 : BWD_SPLIT;
+    out[0] = fu ? BWD_FUSED : ds_possible(desc) ? BWD_DS : keys_possible(desc) ? BWD_SPLIT16 : BWD_SPLIT;
     out[1] = fu ? bwd_fused_rows() : bwd_dkdv_block_rows(D, desc->compute_dtype);
     out[2] = fu ? cdiv(N, out[1]) : main_blocks(desc->batch * desc->heads, N, out[1]);
     out[3] = fu ? 512 : bwd_dkdv_threads(D, desc->compute_dtype);

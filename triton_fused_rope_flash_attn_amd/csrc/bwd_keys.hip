@@ -6,9 +6,12 @@
 // dK = R^T dK-hat * scale, the CLS row bypassing the rotation
 // (_attn_bwd_dk_dv_rope, FA:374-691; FA:647-662).
 //
-// Runs after bwd_dq_kernel, which writes what this kernel stages per query
-// stage: delta, the fp16 rotated rows Q-hat * c2 (c2 = scale * log2 e, its
-// logit operand) and per-row statistics {|dO|_2, max |Q-hat c2|}.  One 8-wave
+// Runs after bwd_dq_kernel (or the stored-dS row pass, bwd_ds.hip), which
+// writes what this kernel stages per query stage: delta, the fp16 rotated rows
+// Q-hat * c2 (c2 = scale * log2 e, its logit operand) and per-row statistics
+// {|dO|_2, max |Q-hat c2|}.  DS (the stored-dS backward): the tile also stores
+// its fp16 sig dS^T blocks, its K-hat * fk rows and the exponent of
+// 1 / (sig fk), the operands of that backward's dQ GEMM.  One 8-wave
 // workgroup per (plane, 128-key tile), the layout of the generic dK/dV kernel
 // (bwd.hip): each wave's K-hat and V rows are MFMA B operands in registers,
 // and the Q-hat / dO rows of each 64-query stage are staged in LDS (rows
@@ -52,7 +55,7 @@ __device__ __forceinline__ const IO* plane_ptr(const void* b, const int64_t* st,
 // ---------------------------------------------------------------------------
 // Key tiles.
 // ---------------------------------------------------------------------------
-template <typename IO>
+template <typename IO, bool DS>
 __global__ void __launch_bounds__(512) bwd_keys_kernel(const BwdParams p) {
   using C = Comp<DT_BF16>;   // dP = dO V and dV = P^T dO
   using H = Comp<DT_F16>;    // logits and dK-hat
@@ -175,6 +178,18 @@ __global__ void __launch_bounds__(512) bwd_keys_kernel(const BwdParams p) {
     kf[s].v = to_f16x8(x);
     vf[s] = C::make(y);
   }
+  // DS: this tile's K-hat * fk rows (rows >= N are zero) and its exponent of
+  // 1 / (sig fk) for the dQ GEMM; sig dS^T is stored per query block below
+  const int KP = p.n_blk * KROWS;
+  if constexpr (DS) {
+    f16* kh = static_cast<f16*>(p.khat) + ((int64_t)plane * KP + kv_first + lr) * D;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) *reinterpret_cast<f16x8*>(kh + 32 * s + 8 * lg) = kf[s].v;
+    if (tid == 0)
+      p.kexp[plane * p.n_blk + kblk] = 254 - (int)(__float_as_uint(sig) >> 23) - (int)(__float_as_uint(fk) >> 23);
+  }
+  const auto rDS = make_rsrc(DS ? static_cast<const f16*>(p.ds_t) + (int64_t)plane * KP * p.nqp : nullptr,
+                             DS ? (unsigned)(KP * p.nqp * 2) : 0u);
 
   f32x4 dvacc[DT], dkacc[DT];
 #pragma unroll
@@ -271,7 +286,7 @@ __global__ void __launch_bounds__(512) bwd_keys_kernel(const BwdParams p) {
   // P and dS of block j, dV += P^T dO, dK-hat += (sig dS)^T Q-hat.  Keys >= N
   // have zero K-hat / V rows: their P is clamped to [0, 1], dS = -P delta is
   // finite and only reaches dK / dV rows that are never stored.
-  auto pdk = [&](int b, int j, const f32x4 (&sacc)[2], const f32x4 (&pacc)[2]) __attribute__((always_inline)) {
+  auto pdk = [&](int b, int qb, int j, const f32x4 (&sacc)[2], const f32x4 (&pacc)[2]) __attribute__((always_inline)) {
     // the transposed operands of the first PF channel tiles are read before
     // the probabilities are formed, and each product then reads the tile PF
     // further on: every product waits for a read issued PF products earlier
@@ -298,6 +313,11 @@ __global__ void __launch_bounds__(512) bwd_keys_kernel(const BwdParams p) {
     const Frag pf = C::make(pv);
     HFrag dsf;
     dsf.v = to_f16x8(dsv);
+    if constexpr (DS) {   // sig dS^T: key kv_first + lr, queries qb + 32j + 8lg ..
+      u32x4 w;
+      __builtin_memcpy(&w, &dsf.v, 16);
+      __builtin_amdgcn_raw_buffer_store_b128(w, rDS, (unsigned)(((kv_first + lr) * p.nqp + qb + 32 * j + 8 * lg) * 2), 0u, 0);
+    }
 #pragma unroll
     for (int d = 0; d < DT; ++d) {
       // A = dO^T / Q-hat^T rows 16d.., k-slot e <-> query 32j + 8lg + e (the P / dS order)
@@ -321,7 +341,7 @@ __global__ void __launch_bounds__(512) bwd_keys_kernel(const BwdParams p) {
       f32x4 sA[2], pA[2], sB[2], pB[2];
       sp(B, j, sA, pA);
       sp(B, min(j + 1, nbj - 1), sB, pB);
-      pdk(B, j, sA, pA);
+      pdk(B, qb, j, sA, pA);
       // the next stage goes into the other buffer (last read in the previous
       // stage, which every wave finished before this stage's barrier), and
       // the stage after it is prefetched (past the last stage: rows >= N)
@@ -330,7 +350,7 @@ __global__ void __launch_bounds__(512) bwd_keys_kernel(const BwdParams p) {
         prefetch(qb + 2 * QS);
       }
       if (j + 1 < nbj) {
-        pdk(B, j + 1, sB, pB);
+        pdk(B, qb, j + 1, sB, pB);
         // the last block's order, which the scheduler otherwise collapses to
         // one read ahead: the 12 reads of its first three channel tiles, then
         // per tile its two products and the 4 reads three tiles on
@@ -382,8 +402,14 @@ hipError_t launch_bwd_keys(const BwdParams& p0, int io, hipStream_t st) {
   BwdParams p = p0;
   p.n_wg = p.B * p.H * p.n_blk;
   switch (io) {
-    case DT_BF16: hipLaunchKernelGGL((bwd_keys_kernel<bf16>), dim3(p.n_wg), dim3(512), 0, st, p); break;
-    case DT_F16: hipLaunchKernelGGL((bwd_keys_kernel<f16>), dim3(p.n_wg), dim3(512), 0, st, p); break;
+    case DT_BF16:
+      if (p.ds_t) hipLaunchKernelGGL((bwd_keys_kernel<bf16, true>), dim3(p.n_wg), dim3(512), 0, st, p);
+      else hipLaunchKernelGGL((bwd_keys_kernel<bf16, false>), dim3(p.n_wg), dim3(512), 0, st, p);
+      break;
+    case DT_F16:
+      if (p.ds_t) hipLaunchKernelGGL((bwd_keys_kernel<f16, true>), dim3(p.n_wg), dim3(512), 0, st, p);
+      else hipLaunchKernelGGL((bwd_keys_kernel<f16, false>), dim3(p.n_wg), dim3(512), 0, st, p);
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

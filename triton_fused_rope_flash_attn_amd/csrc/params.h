@@ -56,6 +56,13 @@ struct BwdParams {
   float* row_stat;     // non-null: per query row {|dO|_2, max |Q-hat * scale * log2(e)|}
                        // [planes * N][2], written by the dQ kernel's first pass; the
                        // key-tile kernel (bwd_keys.hip) then replaces the dK/dV kernel
+  // Stored-dS backward (bwd_ds.hip); ds_t non-null selects it in the key tiles.
+  void* ds_t;          // fp16 sig * dS^T of the key tiles: [planes][n_kt * 128][nqp]
+  void* khat;          // fp16 K-hat * fk of the key tiles: [planes][n_kt * 128][D]
+  int* kexp;           // per key tile: log2 of 1 / (sig * fk), [planes][n_kt]
+  float* dslast;       // non-null: dS of the lone key N - 1 per query row, [planes][N]
+  int nqp;             // dS^T row pitch in elements (N rounded up to 64)
+  int n_kt;            // key tiles per plane
 };
 
 // Launch shapes picked by the tile table (api.hip).
@@ -64,6 +71,8 @@ enum BwdVariant : int {
   BWD_SPLIT = 1,    // dQ kernel (Q-outer, also writes delta) + dK/dV kernel (KV-outer)
   BWD_SPLIT16 = 2,  // dQ kernel + key-tile kernel, both with fp16 dS products
                     // (bwd_keys.hip; with vector access to every tensor, else BWD_SPLIT)
+  BWD_DS = 3,       // row pass + key tiles that store dS + dQ as one GEMM over it
+                    // (bwd_ds.hip; with vector access to every tensor, else BWD_SPLIT16)
 };
 
 // Launchers: return hipSuccess or the launch error.  io/ct are DT_* codes.
@@ -106,6 +115,15 @@ hipError_t launch_bwd_tail_key_merge(const BwdParams& p, int io, int D, int npar
 // p.row_stat (and delta) from the dQ kernel's pass before it.
 constexpr int kKeysRows = 128;
 hipError_t launch_bwd_keys(const BwdParams& p, int io, hipStream_t st);
+// Stored-dS backward (bwd_ds.hip), the key tiles' shapes: the row pass
+// (delta, p.qhat_f, p.row_stat and, with p.dslast, the lone last key's dS and
+// partial dK-hat / dV rows into p.xk_ws, one pair per row tile) before the
+// key tiles, and the dQ GEMM over their stored dS after them.
+constexpr int kDsPrepRows = 64;     // query rows per row-pass workgroup
+constexpr int kDsQueryRows = 256;   // query rows per dQ GEMM workgroup
+constexpr int kDsMaxKeyTiles = 256;  // key tiles per plane (N < 32768, from the 32-bit dS^T offsets)
+hipError_t launch_bwd_ds_prep(const BwdParams& p, int io, hipStream_t st);
+hipError_t launch_bwd_ds_dq(const BwdParams& p, int io, hipStream_t st);
 
 // Whether the forward block kernel computes a single tail row itself
 // (FwdParams::x_rows = 1) instead of launch_fwd_tail: fp16 logit operands with
