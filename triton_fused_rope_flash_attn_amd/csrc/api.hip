@@ -317,8 +317,8 @@ int64_t bwd_caller_ws(const farope_attn_desc* d) {
   return t > s ? t : s;
 }
 
-// Stored-dS backward: row pass, key tiles (storing dS), dQ GEMM, and the
-// merge of the lone last key's partial rows.
+// Stored-dS backward: row pass, key tiles (storing dS), dQ GEMM (which also
+// merges the lone last key's partial dK / dV rows).
 int ds_pass(BwdParams p, const farope_attn_desc* d, float* ws, hipStream_t st) {
   const DsWs w = ds_ws(d);
   const int planes = p.B * p.H, N = p.N;
@@ -335,10 +335,7 @@ int ds_pass(BwdParams p, const farope_attn_desc* d, float* ws, hipStream_t st) {
   FAROPE_TRY(launch_rc(launch_bwd_ds_prep(p, d->io_dtype, st)));
   p.n_blk = p.n_kt;
   FAROPE_TRY(launch_rc(launch_bwd_keys(p, d->io_dtype, st)));
-  FAROPE_TRY(launch_rc(launch_bwd_ds_dq(p, d->io_dtype, st)));
-  if (last)
-    FAROPE_TRY(launch_rc(launch_bwd_tail_key_merge(p, d->io_dtype, kDsD, cdiv(N, kDsPrepRows), st)));
-  return FAROPE_OK;
+  return launch_rc(launch_bwd_ds_dq(p, d->io_dtype, st));
 }
 
 int bwd_impl(const farope_attn_desc* desc, const void* q, const int64_t q_stride[4],

@@ -14,7 +14,8 @@
 // tiles stage; with one key past the full key tiles, that key's dS per row and
 // the tile's partial dK-hat / dV rows), the key tiles (dK, dV; they store
 // sig dS^T and K-hat * fk in fp16 with each tile's exponent of 1 / (sig fk)),
-// then bwd_ds_dq_kernel (dQ) and the merge of the last key's partial rows.
+// then bwd_ds_dq_kernel (dQ; the first tile of each plane also adds up the
+// last key's partial rows into its dK / dV).
 #include <type_traits>
 
 #include "common.h"
@@ -188,11 +189,14 @@ __global__ void __launch_bounds__(256) bwd_ds_prep_kernel(const BwdParams p, int
 // K-hat [64][128 + 8], rows padded by 16 bytes) from registers loaded two
 // blocks ahead, and both operands are read transposed (ds_read_b64_tr_b16).
 // ---------------------------------------------------------------------------
-template <typename IO>
-__global__ void __launch_bounds__(512) bwd_ds_dq_kernel(const BwdParams p, int n_qt) {
+template <typename IO, int QR, int NW>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+bwd_ds_dq_kernel(const BwdParams p, int n_qt) {
   using H = Comp<DT_F16>;
   using HFrag = H::Frag;
-  constexpr int D = kDsD, D2 = D / 2, QR = kDsQueryRows, KB = 64, NT = 512;
+  constexpr int D = kDsD, D2 = D / 2, KB = 64, NT = NW * 64;
+  constexpr int WQ = QR / 64;   // waves along the queries (64 each); NW / WQ along the channels
+  static_assert(WQ * (D / 64) == NW, "wave tiling: 64 x 64 per wave");
   constexpr int LDS_ = QR + 8, LDK = D + 8;
   constexpr int SI = KB * QR / 8 / NT, KI = KB * D / 8 / NT;   // 16-byte units per thread
   static_assert(SI * NT * 8 == KB * QR && KI * NT * 8 == KB * D && kKeysRows % KB == 0, "tile shape");
@@ -207,7 +211,7 @@ __global__ void __launch_bounds__(512) bwd_ds_dq_kernel(const BwdParams p, int n
   const int tid = thread_id();
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, lr = lane & 15, lg = lane >> 4;
-  const int qw = 64 * (wave & 3), cw = 64 * (wave >> 2);
+  const int qw = 64 * (wave % WQ), cw = 64 * (wave / WQ);
 
   const int* __restrict__ kexp = p.kexp + (int64_t)plane * n_kt;
   int emax = kexp[0];
@@ -222,7 +226,8 @@ __global__ void __launch_bounds__(512) bwd_ds_dq_kernel(const BwdParams p, int n
   // staging units: dS^T row sr + 16 i, queries q0 + 8 sc ..; K-hat row kr + 32 i, channels 8 kc ..
   // (the key tiles write the columns below N rounded up to 32, zeros past N;
   // later ones are staged as zeros: their lane offset is past the range)
-  const int sr = tid >> 5, sc = tid & 31, kr = tid >> 4, kc = tid & 15;
+  constexpr int SC = QR / 8, SR = NT / SC, KR = NT / 16;   // 16-byte units per dS^T row; rows per pass
+  const int sr = tid / SC, sc = tid % SC, kr = tid >> 4, kc = tid & 15;
   const unsigned svo = q0 + 8 * sc < round_up32(N) ? (unsigned)((sr * NQP + q0 + 8 * sc) * 2) : 0x80000000u;
   const unsigned kvo = (unsigned)((kr * D + 8 * kc) * 2);
   u32x4 ps[2][SI], pk[2][KI];
@@ -232,15 +237,15 @@ __global__ void __launch_bounds__(512) bwd_ds_dq_kernel(const BwdParams p, int n
     const unsigned bs = (unsigned)(kb * KB * NQP * 2), bk = (unsigned)(kb * KB * D * 2);
 #pragma unroll
     for (int i = 0; i < SI; ++i)
-      ps[s][i] = __builtin_amdgcn_raw_buffer_load_b128(rS, svo + (unsigned)(i * 16 * NQP * 2), bs, 0);
+      ps[s][i] = __builtin_amdgcn_raw_buffer_load_b128(rS, svo + (unsigned)(i * SR * NQP * 2), bs, 0);
 #pragma unroll
     for (int i = 0; i < KI; ++i)
-      pk[s][i] = __builtin_amdgcn_raw_buffer_load_b128(rK, kvo + (unsigned)(i * 32 * D * 2), bk, 0);
+      pk[s][i] = __builtin_amdgcn_raw_buffer_load_b128(rK, kvo + (unsigned)(i * KR * D * 2), bk, 0);
   };
   auto commit = [&](auto setc, auto bufc, int kb) __attribute__((always_inline)) {
     constexpr int s = decltype(setc)::value, b = decltype(bufc)::value;
 #pragma unroll
-    for (int i = 0; i < SI; ++i) *reinterpret_cast<u32x4*>(&sS[b][(sr + 16 * i) * LDS_ + 8 * sc]) = ps[s][i];
+    for (int i = 0; i < SI; ++i) *reinterpret_cast<u32x4*>(&sS[b][(sr + SR * i) * LDS_ + 8 * sc]) = ps[s][i];
     // this tile's K-hat rows to the plane's exponent (unconditionally: a
     // branch here makes the compiler wait for every load in flight)
     const f16 f = sF[min(kb / (kKeysRows / KB), n_kt - 1)];
@@ -251,7 +256,7 @@ __global__ void __launch_bounds__(512) bwd_ds_dq_kernel(const BwdParams p, int n
       pk[s][i] = __builtin_bit_cast(u32x4, h);
     }
 #pragma unroll
-    for (int i = 0; i < KI; ++i) *reinterpret_cast<u32x4*>(&sK[b][(kr + 32 * i) * LDK + 8 * kc]) = pk[s][i];
+    for (int i = 0; i < KI; ++i) *reinterpret_cast<u32x4*>(&sK[b][(kr + KR * i) * LDK + 8 * kc]) = pk[s][i];
   };
 
   f32x4 acc[4][4];   // [channel block][query block]
@@ -347,6 +352,29 @@ __global__ void __launch_bounds__(512) bwd_ds_dq_kernel(const BwdParams p, int n
       }
     }
   }
+  // the lone last key's dK / dV (the plane's first tile): the row pass's
+  // partial rows added in order, dK-hat scaled and rotated back
+  if (p.dslast && qt == 0 && tid < D / 4) {
+    const int n_pt = (N + kDsPrepRows - 1) / kDsPrepRows, kc = N - 1;
+    const float* w = p.xk_ws + (int64_t)plane * n_pt * (2 * D);
+    float xk[4] = {}, xv[4] = {};
+    for (int b = 0; b < n_pt; ++b) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(w + b * 2 * D + 4 * tid);
+      const f32x4 v = *reinterpret_cast<const f32x4*>(w + b * 2 * D + D + 4 * tid);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xk[e] += a[e];
+        xv[e] += v[e];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) xk[e] *= p.scale;
+    rope_unrotate4(xk, tab, kc + shift, D2, 2 * tid);
+    IO* DK = const_cast<IO*>(plane_ptr<IO>(p.dk, p.sdk, plane, p.H)) + (int64_t)kc * p.sdk[2];
+    IO* DV = const_cast<IO*>(plane_ptr<IO>(p.dv, p.sdv, plane, p.H)) + (int64_t)kc * p.sdv[2];
+    store4(DK + 4 * tid, 1, true, xk);
+    store4(DV + 4 * tid, 1, true, xv);
+  }
 }
 
 hipError_t launch_bwd_ds_prep(const BwdParams& p, int io, hipStream_t st) {
@@ -362,11 +390,12 @@ hipError_t launch_bwd_ds_prep(const BwdParams& p, int io, hipStream_t st) {
 
 hipError_t launch_bwd_ds_dq(const BwdParams& p0, int io, hipStream_t st) {
   BwdParams p = p0;
-  const int n_qt = (p.N + kDsQueryRows - 1) / kDsQueryRows;
+  constexpr int QR = kDsQueryRows, NW = QR / 64 * 2;
+  const int n_qt = (p.N + QR - 1) / QR;
   p.n_wg = p.B * p.H * n_qt;
   switch (io) {
-    case DT_BF16: hipLaunchKernelGGL((bwd_ds_dq_kernel<bf16>), dim3(p.n_wg), dim3(512), 0, st, p, n_qt); break;
-    case DT_F16: hipLaunchKernelGGL((bwd_ds_dq_kernel<f16>), dim3(p.n_wg), dim3(512), 0, st, p, n_qt); break;
+    case DT_BF16: hipLaunchKernelGGL((bwd_ds_dq_kernel<bf16, QR, NW>), dim3(p.n_wg), dim3(NW * 64), 0, st, p, n_qt); break;
+    case DT_F16: hipLaunchKernelGGL((bwd_ds_dq_kernel<f16, QR, NW>), dim3(p.n_wg), dim3(NW * 64), 0, st, p, n_qt); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -118,7 +118,8 @@ hipError_t launch_bwd_keys(const BwdParams& p, int io, hipStream_t st);
 // Stored-dS backward (bwd_ds.hip), the key tiles' shapes: the row pass
 // (delta, p.qhat_f, p.row_stat and, with p.dslast, the lone last key's dS and
 // partial dK-hat / dV rows into p.xk_ws, one pair per row tile) before the
-// key tiles, and the dQ GEMM over their stored dS after them.
+// key tiles, and the dQ GEMM over their stored dS after them (with p.dslast
+// it also sums those partial rows into the last key's dK and dV).
 constexpr int kDsPrepRows = 64;     // query rows per row-pass workgroup
 constexpr int kDsQueryRows = 256;   // query rows per dQ GEMM workgroup
 constexpr int kDsMaxKeyTiles = 256;  // key tiles per plane (N < 32768, from the 32-bit dS^T offsets)
