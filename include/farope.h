@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define FAROPE_ABI_VERSION 4
+#define FAROPE_ABI_VERSION 5
 
 typedef enum farope_dtype {
   FAROPE_F32 = 0,

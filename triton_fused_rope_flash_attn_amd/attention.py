@@ -150,8 +150,9 @@ def attn_bwd(
     dv = torch.empty((B, H, N, D), dtype=v.dtype, device=q.device)
     desc = _lib.make_desc(B, H, N, D, n_pos, has_cls, _lib.DTYPE_CODE[q.dtype], compute_dtype,
                           softmax_scale)
-    # delta rows (+ the dQ tiles' partial rows of a lone last key, when used);
-    # none for the one-pass backward, which keeps delta on chip
+    # the backward's workspace (delta rows, and at head_dim 128 the rotated Q
+    # rows, row statistics and stored dS^T of the key tiles); none for the
+    # one-pass backward, which keeps delta on chip
     ws = _lib.bwd_workspace_elems(desc)
     delta = torch.empty(ws, dtype=torch.float32, device=q.device) if ws else None
     if o_res.numel() and (o_res.shape != q.shape or o_res.dtype != q.dtype or not o_res.is_contiguous()):
