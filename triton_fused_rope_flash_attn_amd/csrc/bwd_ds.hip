@@ -25,6 +25,7 @@ namespace farope {
 
 namespace {
 constexpr int kDsD = 128;
+constexpr int kCachePolicyNT = 2;   // buffer instruction cache-policy bit nt (gfx950)
 
 template <typename IO>
 __device__ __forceinline__ const IO* plane_ptr(const void* b, const int64_t* st, int plane, int H) {
@@ -233,11 +234,13 @@ bwd_ds_dq_kernel(const BwdParams p, int n_qt) {
   u32x4 ps[2][SI], pk[2][KI];
   auto load = [&](auto setc, int kb) __attribute__((always_inline)) {
     constexpr int s = decltype(setc)::value;
-    // past the last block: offsets beyond the range, zeros (never committed)
+    // past the last block: offsets beyond the range, zeros (never committed).
+    // dS^T is read once: non-temporal loads (cache policy nt), so it does not
+    // displace the K-hat rows the plane's other query tiles re-read from L2
     const unsigned bs = (unsigned)(kb * KB * NQP * 2), bk = (unsigned)(kb * KB * D * 2);
 #pragma unroll
     for (int i = 0; i < SI; ++i)
-      ps[s][i] = __builtin_amdgcn_raw_buffer_load_b128(rS, svo + (unsigned)(i * SR * NQP * 2), bs, 0);
+      ps[s][i] = __builtin_amdgcn_raw_buffer_load_b128(rS, svo + (unsigned)(i * SR * NQP * 2), bs, kCachePolicyNT);
 #pragma unroll
     for (int i = 0; i < KI; ++i)
       pk[s][i] = __builtin_amdgcn_raw_buffer_load_b128(rK, kvo + (unsigned)(i * KR * D * 2), bk, 0);
