@@ -210,6 +210,30 @@ def test_ragged_and_variant_shapes(side, has_cls, D):
     _compare(f"side{side}-cls{int(has_cls)}-D{D}", ours, ref, out_dtype=torch.bfloat16, other=other)
 
 
+@pytest.mark.parametrize("case", ["n256", "tile_scales"])
+def test_stored_ds_backward(case):
+    """The stored-dS backward (variant 3: head_dim 128, bf16 compute, 16-bit I/O):
+    N = 256, no CLS (two full key tiles, no lone key, no ragged tile); and N = 257
+    with V scaled by 2^-12 on the first 128 keys, so that the key tiles bound |dS|
+    differently, store it at different powers of two (their exponents differ) and
+    the dQ GEMM stages each tile's K-hat rows at its own scale."""
+    B, H, D = 2, 3, 128
+    side, has_cls = (16, False) if case == "n256" else (16, True)
+    N = side * side + int(has_cls)
+    desc = _lib.make_desc(B, H, N, D, N - int(has_cls), has_cls, _lib.BF16, _lib.BF16, 1 / math.sqrt(D))
+    assert _lib.tile_config(desc, 1)[0] == 3
+    cfg = dict(B=B, H=H, side=side, has_cls=has_cls, D=D, dtype=torch.bfloat16, scale=1.0, dout="randn")
+    q, k, v, do = make_inputs(cfg, DEV, seed=7)
+    if case == "tile_scales":
+        v = v.clone()
+        v[:, :, :128] *= 2.0 ** -12   # exact in bf16
+    _say(f"case stored-ds {case}: N={N}")
+    table = CosSinTable(ROPE_BASE, side, D, device=DEV)
+    ours = _run_ours(q, k, v, do, table, has_cls)
+    ref = _ref(q, k, v, do, table, has_cls)
+    _compare(f"stored-ds-{case}-N{N}", ours, ref, out_dtype=torch.bfloat16)
+
+
 @pytest.mark.parametrize(
     "side,has_cls,D,B,H,io",
     [(16, True, 128, 2, 3, "bf16"), (16, True, 32, 2, 3, "bf16"), (16, True, 256, 2, 3, "bf16"),
