@@ -122,7 +122,8 @@ size_t farope_attn_residual_elems(const farope_attn_desc* desc);
  * each query row's {|dO|_2, max |Q-hat * scale * log2(e)|}, from which the
  * key-tile kernel fixes its fp16 operand scalings.  At the stored-dS shapes
  * (16-bit I/O, bf16 compute, head_dim 128, at most one key past the 128-key
- * tiles) the larger of that and the stored-dS layout, whose parts each start
+ * tiles, and a dS^T plane of at most 16 Q planes: seq_len up to about 2k) the
+ * larger of that and the stored-dS layout, whose parts each start
  * on a 256-byte boundary: the delta rows; with a lone last key one partial
  * dK / dV row pair per 64-row tile; the fp16 rotated Q rows; the row
  * statistics; with a lone last key its dS per query row; one int32 exponent

@@ -85,7 +85,8 @@ def test_tile_table(lib, N, D, has_cls, fwd_var, fwd_items, bwd_var):
 
 def _ds_elems(B, H, N, D):
     """Workspace of the stored-dS backward (None where it does not apply: more
-    than one key past the 128-key tiles), in fp32 elements, each part from a
+    than one key past the 128-key tiles, or a dS^T plane larger than 16 Q
+    planes), in fp32 elements, each part from a
     64-float boundary: delta rows; with a lone last key one partial dK / dV
     row pair per 64-row tile; fp16 Q-hat rows; {|dO|, max |Q-hat|} per row;
     with a lone last key its dS per row; an int32 exponent per key tile; fp16
@@ -95,8 +96,10 @@ def _ds_elems(B, H, N, D):
     t = r if N >= 128 and 0 < r <= 8 else 0
     if t > 1:
         return None
-    planes, rows = B * H, B * H * N
     n_kt = N // 128 if t else -(-N // 128)
+    if n_kt * 128 * ((N + 63) // 64 * 64) > 16 * N * D:   # dS^T plane > 16 Q planes
+        return None
+    planes, rows = B * H, B * H * N
     kp, n_pt, nqp = n_kt * 128, -(-N // 64), (N + 63) // 64 * 64
 
     def al(x):
@@ -125,6 +128,7 @@ def _ds_elems(B, H, N, D):
         (2, 3, 257, 128, _lib.F16, _lib.F16, 0, False),                 # fp16 compute
         (2, 3, 1100, 128, _lib.BF16, _lib.BF16, 0, True),               # 76 rows past the blocks
         (2, 3, 3970, 128, _lib.BF16, _lib.BF16, 0, True),               # dQ blocks leave 130 rows
+     (1, 2, 4097, 128, _lib.BF16, _lib.BF16, 16 * 2 * 128, True),    # N = 4097: split path (dS^T > 16 Q planes)
         (1, 2, 3844, 128, _lib.BF16, _lib.BF16, 0, False),              # 4 tail rows: tail kernel
     ],
 )

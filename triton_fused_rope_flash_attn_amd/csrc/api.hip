@@ -269,7 +269,8 @@ int64_t split_caller_ws(const farope_attn_desc* d) {
 
 // The stored-dS backward (bwd_ds.hip): the key tiles' shapes (16-bit I/O, bf16
 // compute, head_dim 128) with at most one key past the full key tiles, and a
-// dS^T plane that 32-bit offsets address.  (Vector access to every tensor is
+// dS^T plane of at most 16 Q planes (N up to about 2k; its workspace grows
+// with N^2, the split path's with N).  (Vector access to every tensor is
 // checked at the call.)
 constexpr int kDsD = 128;
 int ds_pitch(int N) { return (N + 63) & ~63; }   // 128-byte rows
@@ -279,7 +280,7 @@ bool ds_possible(const farope_attn_desc* d) {
   const int planes = d->batch * d->heads, N = d->seq_len;
   if (tail_of(planes, N, kKeysRows) > 1) return false;
   const int64_t n_kt = main_blocks(planes, N, kKeysRows), kp = n_kt * kKeysRows;
-  return n_kt <= kDsMaxKeyTiles && kp * ds_pitch(N) * 2 < ((int64_t)1 << 31);
+  return n_kt <= kDsMaxKeyTiles && kp * ds_pitch(N) <= 16 * (int64_t)N * kDsD;
 }
 // Its workspace, in fp32 elements, each part from a 256-byte boundary: delta
 // rows; (lone last key) one partial dK-hat / dV row pair per row-pass tile;
