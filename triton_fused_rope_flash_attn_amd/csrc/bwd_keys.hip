@@ -360,6 +360,8 @@ __global__ void __launch_bounds__(512) bwd_keys_kernel(const BwdParams p) {
           __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
           if (d + 3 < DT) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
         }
+        // (DS: the block's dS store after its products; first, it delays them)
+        if constexpr (DS) __builtin_amdgcn_sched_group_barrier(0x040, 1, 0);
       }
     }
   };
