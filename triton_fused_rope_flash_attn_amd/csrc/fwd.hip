@@ -102,9 +102,9 @@ fwd_kernel(const FwdParams p) {
   constexpr int KS = D / 32;          // k-steps of 32 channels
   constexpr int DT = D / 16;          // 16-channel output subtiles
   constexpr int D2 = D / 2;
-  // K-hat / V row padding: 16 bytes, or 32 with fp16 logits at D >= 128, where
-  // the K-hat fragment reads (16 consecutive rows, 16 bytes each) then run at
-  // the conflict-free rate (HiRes forward -2 us, bit-identical)
+  // K-hat / V row padding: 16 bytes, or 32 with fp16 logits at D >= 128 (the
+  // pitch at which 16-byte reads of 16 consecutive rows, the K-hat fragment
+  // reads, measured conflict-free in isolation; HiRes forward -2 us)
   constexpr int PADE = (FS && D >= 128) ? 16 : 16 / sizeof(S);
   constexpr int LDK = D + PADE;       // K-hat row pitch (elements)
   constexpr int LDV = KC + 16;        // V^T row pitch (elements; see vswz)
