@@ -314,8 +314,14 @@ bwd_plane_kernel(const BwdParams p) {
   };
   auto load_kq = [&]() __attribute__((always_inline)) {
     if constexpr (KQREG) {
+      // the two lane addresses once for all blocks (ka_tr would form them
+      // again per block from its opaque lane copy)
+      const int lane = opaque(tid & 63), lr = lane & 15, lg = lane >> 4;
+      const int r0 = 8 * lg + (lr >> 2);
+      const S* ka0 = &sK[sw64(r0, 16 * dd + 4 * (lr & 3))];
+      const S* ka1 = &sK[sw64(r0 + 4, 16 * dd + 4 * (lr & 3))];
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) kq[kb] = ka_tr(kb);
+      for (int kb = 0; kb < NKB; ++kb) kq[kb] = C::tr(ka0 + 32 * kb * LD, ka1 + 32 * kb * LD);
     }
   };
 
@@ -389,8 +395,11 @@ bwd_plane_kernel(const BwdParams p) {
   // products and probabilities are skipped: its P and dS fragment slots are
   // zero for the dV / dK products, and its dS^T columns are left as they are,
   // because they only reach dQ rows >= N, which are never stored.
-  auto sweep_keys = [&](int buf, bool live1) __attribute__((always_inline)) {
+  // F0 (a std::bool_constant): the plane's first stage, whose dV / dK
+  // products start from zero accumulators instead of adding to them.
+  auto sweep_keys = [&](int buf, bool live1, auto f0c) __attribute__((always_inline)) {
     constexpr int NUA = 2;
+    constexpr bool F0 = decltype(f0c)::value;
     const S* q = &sQ[buf][0];
     const S* g = &sG[buf][0];
     S* ds = &sdS[buf][0];
@@ -468,8 +477,8 @@ bwd_plane_kernel(const BwdParams p) {
         const Frag aq = C::tr(q + o0, q + o1);
 #pragma unroll
         for (int u = 0; u < NUA; ++u) {
-          dvacc[u][d] = C::mma(ag, pf[u], dvacc[u][d]);
-          dkacc[u][d] = C::mma(aq, dsf[u], dkacc[u][d]);
+          dvacc[u][d] = C::mma(ag, pf[u], F0 ? f32x4{0.f, 0.f, 0.f, 0.f} : dvacc[u][d]);
+          dkacc[u][d] = C::mma(aq, dsf[u], F0 ? f32x4{0.f, 0.f, 0.f, 0.f} : dkacc[u][d]);
         }
       }
     }
@@ -509,6 +518,13 @@ bwd_plane_kernel(const BwdParams p) {
   }
   // the table copy and the zeroed rows are visible
   lds_barrier();
+  // The first stage of every plane sets the dV / dK accumulators of a wave
+  // with keys < N; a wave without any keeps whatever they hold (its stores
+  // fall past N and are dropped).  Defined once here.
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int d = 0; d < 4; ++d) dvacc[u][d] = dkacc[u][d] = f32x4{0.f, 0.f, 0.f, 0.f};
   while (plane >= 0) {
     const int nxt = item_of(it + 1);
     const auto rdq = rsrc(p.dq, p.sdq, plane);   // (VEC)
@@ -525,10 +541,6 @@ bwd_plane_kernel(const BwdParams p) {
     // this plane writes it
     lds_barrier();
     load_kq();
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int d = 0; d < 4; ++d) dvacc[u][d] = dkacc[u][d] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // One query stage.  The stage loop runs two stages per trip, so the LDS
     // buffer index BUF is a compile-time constant and the buffers' addresses
@@ -553,7 +565,7 @@ bwd_plane_kernel(const BwdParams p) {
         prefetch(tp, rs, last ? 0 : qb + QS);
       }
       if constexpr (!FIRST) dq(plane, rdq, st - 1, buf ^ 1);
-      if (nu > 0) sweep_keys(buf, qb + 16 < N);
+      if (nu > 0) sweep_keys(buf, qb + 16 < N, firstc);
     };
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
