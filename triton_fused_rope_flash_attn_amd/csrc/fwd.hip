@@ -446,6 +446,53 @@ fwd_kernel(const FwdParams p) {
   };
   LFrag qf[QT][KS];
   bool xi = false;   // XR: this item pass also computes the plane's last row
+  // Q rows loaded at the item start (!kQpf) with vector access: through
+  // descriptors over the plane's rows (rows >= N read 0; lanes with no part
+  // of the plane's last row read past the range), every load of the item's
+  // Q-hat fragments, their table values and (XR) the plane's last row goes
+  // out before the first is used, so the item start waits once for all of
+  // them (a load per fragment behind a row test waited once per fragment,
+  // each time also for every store still in flight).
+  constexpr bool kQdesc = !kQpf && VEC;
+  Raw8<IO> qld[kQdesc ? QT : 1][kQdesc ? KS : 1];
+  float qtb[kQdesc ? QT : 1][kQdesc ? KS : 1][kQdesc ? 8 : 1];
+  Raw8<IO> xld;
+  float xtb[8];
+  auto load_q = [&](int plane, int qb) __attribute__((always_inline)) {
+    if constexpr (kQdesc) {
+      const auto rQ = rsrc(p.q, p.sq, plane);
+      const auto rT = make_rsrc(p.rope, (unsigned)((N + shift) * D * 4));
+#pragma unroll
+      for (int t = 0; t < QT; ++t) {
+        const int row = (qb * NW * QT + t * NW + wave) * 16 + lr;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const int c0 = 32 * s + 8 * lg;
+          qld[t][s] = buf_load8<IO>(rQ, (unsigned)((row * (int)p.sq[2] + c0) * (int)ES), 0u);
+          const unsigned to = (unsigned)(((row + shift) * D + c0) * 4);
+          const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rT, to, 0u, 0);
+          const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(rT, to + 16, 0u, 0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            qtb[t][s][e] = __uint_as_float(a[e]);
+            qtb[t][s][4 + e] = __uint_as_float(b[e]);
+          }
+        }
+      }
+      if constexpr (XR) {
+        const bool xl = wave == 0 && lane < D / 8;
+        xld = buf_load8<IO>(rQ, xl ? (unsigned)(((N - 1) * (int)p.sq[2] + 8 * lane) * (int)ES) : 0x80000000u, 0u);
+        const unsigned to = xl ? (unsigned)(((N - 1 + shift) * D + 8 * lane) * 4) : 0x80000000u;
+        const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rT, to, 0u, 0);
+        const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(rT, to + 16u, 0u, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          xtb[e] = __uint_as_float(a[e]);
+          xtb[4 + e] = __uint_as_float(b[e]);
+        }
+      }
+    }
+  };
   int npass = 0;     // item passes so far (a rescaled pass counts again)
   auto commit_q = [&](int plane, int qb) __attribute__((always_inline)) {
 #pragma unroll
@@ -453,7 +500,10 @@ fwd_kernel(const FwdParams p) {
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         float x[8];
-        if constexpr (!kQpf) {
+        if constexpr (kQdesc) {
+          unpack8(qld[t][s], x);
+          rope_rotate8(x, qtb[t][s]);
+        } else if constexpr (!kQpf) {
           const int row = (qb * NW * QT + t * NW + wave) * 16 + lr;
           const int c0 = 32 * s + 8 * lg;
           float cs[8];
@@ -488,11 +538,11 @@ fwd_kernel(const FwdParams p) {
       }
     if constexpr (XR) {
       if (xi && wave == 0 && lane < D / 8) {
+        static_assert(kQdesc, "the last row rides along vector-access items only");
         const int c0 = 8 * opaque(lane);
-        float x[8], cs[8];
-        unpack8(load_raw8(plane_base(p.q, p.sq, plane) + (N - 1) * p.sq[2] + c0, 1, true), x);
-        rope_load4(p.rope, N - 1 + shift, D2, c0 / 2, cs);
-        rope_rotate8(x, cs);
+        float x[8];
+        unpack8(xld, x);   // (row N - 1, channels c0 .. c0 + 7)
+        rope_rotate8(x, xtb);
         const float qs = c2 * fq;
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] *= qs;
@@ -987,6 +1037,7 @@ fwd_kernel(const FwdParams p) {
       // plane's launch iteration, so the extra rows spread over workgroups
       xi = p.x_rows != 0 && qb == (plane / max(1, p.n_wg / p.n_blk)) % p.n_blk;
     }
+    if constexpr (kQdesc) load_q(plane, qb);
     commit_q(plane, qb);
     int nt = 0;   // active subtiles of this wave: a prefix t < nt (wave-uniform)
 #pragma unroll
