@@ -628,8 +628,8 @@ bwd_plane_kernel(const BwdParams p) {
             xk[2 + k] = rk[1];
           }
           const int ch = 16 * (d0 + (lg & 1)) + 4 * (lg & 2);
-          __builtin_amdgcn_raw_buffer_store_b128(xv, rdV, boff(p.sdv, row, ch), 0u, 0);
-          __builtin_amdgcn_raw_buffer_store_b128(xk, rdK, boff(p.sdk, row, ch), 0u, 0);
+          buf_store16(xv, rdV, boff(p.sdv, row, ch), 0u);
+          buf_store16(xk, rdK, boff(p.sdk, row, ch), 0u);
         }
       }
     } else {

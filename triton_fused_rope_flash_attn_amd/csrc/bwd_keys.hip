@@ -316,7 +316,7 @@ __global__ void __launch_bounds__(512) bwd_keys_kernel(const BwdParams p) {
     if constexpr (DS) {   // sig dS^T: key kv_first + lr, queries qb + 32j + 8lg ..
       u32x4 w;
       __builtin_memcpy(&w, &dsf.v, 16);
-      __builtin_amdgcn_raw_buffer_store_b128(w, rDS, (unsigned)(((kv_first + lr) * p.nqp + qb + 32 * j + 8 * lg) * 2), 0u, 0);
+      buf_store16(w, rDS, (unsigned)(((kv_first + lr) * p.nqp + qb + 32 * j + 8 * lg) * 2), 0u);
     }
 #pragma unroll
     for (int d = 0; d < DT; ++d) {

@@ -154,6 +154,19 @@ __device__ __forceinline__ Raw8<IO> buf_load8(__amdgpu_buffer_rsrc_t r, unsigned
   return x;
 }
 
+// 16-byte buffer store.  A buffer store reads its data VGPRs after it
+// issues, so a VALU write to them needs a wait state in between; the
+// compiler inserts it only when the store's soffset is an inline constant,
+// and with an SGPR soffset it can place the write directly behind the store,
+// which then stores the new value (measured on gfx950: dK rows of the
+// one-pass backward with fp32 I/O changed from run to run).  The s_nop takes
+// the data as an operand: as a side-effecting statement it stays behind the
+// store, and the registers cannot be rewritten before it.
+__device__ __forceinline__ void buf_store16(u32x4 w, __amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff) {
+  __builtin_amdgcn_raw_buffer_store_b128(w, r, voff, soff, 0);
+  asm volatile("s_nop 0" : : "v"(w));
+}
+
 // 4 elements (converted to IO) at byte offset voff + soff
 template <typename IO>
 __device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff,
@@ -169,7 +182,7 @@ __device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, unsigned vo
   } else {
     u32x4 w;
     __builtin_memcpy(&w, x, 16);
-    __builtin_amdgcn_raw_buffer_store_b128(w, r, voff, soff, 0);
+    buf_store16(w, r, voff, soff);
   }
 }
 

@@ -1011,7 +1011,7 @@ fwd_kernel(const FwdParams p) {
             w[2 + k] = r[1];
           }
           const int ch = 16 * (d0 + (lg & 1)) + cbase;
-          __builtin_amdgcn_raw_buffer_store_b128(w, rO, (unsigned)((orow[t] * (int)p.so[2] + ch) * (int)ES), 0u, 0);
+          buf_store16(w, rO, (unsigned)((orow[t] * (int)p.so[2] + ch) * (int)ES), 0u);
           if constexpr (RES) {
             u32x4 wr;
 #pragma unroll
@@ -1021,7 +1021,7 @@ fwd_kernel(const FwdParams p) {
               wr[2 + k] = r[1];
             }
             // empty range (stores dropped) when there is no residual buffer
-            __builtin_amdgcn_raw_buffer_store_b128(wr, rR, (unsigned)((orow[t] * D + ch) * (int)ES), 0u, 0);
+            buf_store16(wr, rR, (unsigned)((orow[t] * D + ch) * (int)ES), 0u);
           }
         }
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(olse[t]), rL,

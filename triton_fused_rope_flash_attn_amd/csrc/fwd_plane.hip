@@ -355,7 +355,7 @@ __global__ void __launch_bounds__(kFpW * 64) fwd_plane_kernel(const FwdParams p)
           w[k] = r[0];
           w[2 + k] = r[1];
         }
-        __builtin_amdgcn_raw_buffer_store_b128(w, rO, ov + 32u * d0, os, 0);
+        buf_store16(w, rO, ov + 32u * d0, os);
       }
       // LSE of row 16t + lr from lane group 0 (the others address past row
       // N - 1: outside the range)
