@@ -840,6 +840,18 @@ fwd_kernel(const FwdParams p) {
   auto blk_out = [&](auto maskc, const VS* __restrict__ cV, int kvb, int j, const SAcc& sacc)
       __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(maskc)::value;
+    // fp16 logits (vector access): the first kVPre V^T fragments are read before
+    // its softmax, so that their LDS latency passes under it (the compiler
+    // otherwise issues each read next to its product and waits for it there;
+    // 4 fit the register budget: HiRes forward -6 us)
+    constexpr int kVPre = (TRV && FS && VEC) ? 4 : 0;
+    VFrag vpre[kVPre > 0 ? kVPre : 1];
+    if constexpr (kVPre > 0) {
+#pragma unroll
+      for (int d = 0; d < kVPre; ++d)
+        vpre[d] = VC::tr(cV + (32 * j + vr0) * LDK + 16 * d + 4 * (lr & 3), cV + (32 * j + vr1) * LDK + 16 * d + 4 * (lr & 3));
+      __builtin_amdgcn_sched_barrier(0);
+    }
     // ---- online softmax; lane holds keys kvb + 32j + 8lg + (0..7) of its row ----
     const int lim = N - (kvb + 32 * j + 8 * lg);   // keys e < lim are valid (MASKED only)
     VFrag pf[QT];
@@ -888,12 +900,16 @@ fwd_kernel(const FwdParams p) {
     for (int d = 0; d < DT; ++d) {
       // A = V^T rows 16d.., k-slot e <-> key 32j + 8lg + e (the P^T order)
       VFrag a;
-      if constexpr (TRV)
-        a = VC::tr(cV + (32 * j + vr0) * LDK + 16 * d + 4 * (lr & 3), cV + (32 * j + vr1) * LDK + 16 * d + 4 * (lr & 3));
-      else if constexpr (VROW)
+      if constexpr (TRV) {
+        if (d < kVPre)
+          a = vpre[d < kVPre ? d : 0];
+        else
+          a = VC::tr(cV + (32 * j + vr0) * LDK + 16 * d + 4 * (lr & 3), cV + (32 * j + vr1) * LDK + 16 * d + 4 * (lr & 3));
+      } else if constexpr (VROW) {
         a = vrow_frag(cV, j, d);
-      else
+      } else {
         a = C::lds(&cV[(16 * d + lr) * LDV + vswz(16 * d + lr, 32 * j + 8 * lg)]);
+      }
 #pragma unroll
       for (int t = 0; t < QT; ++t) oacc[t][d] = VC::mma(a, pf[t], oacc[t][d]);
     }
