@@ -1240,6 +1240,48 @@ fwd_kernel(const FwdParams p) {
         const float l = group4_sum(l_run[t]);
         const int row = (qb * NW * QT + t * NW + wave) * 16 + lr;
         const float inv = __builtin_amdgcn_rcpf(l) * ifv;
+        if constexpr (sizeof(IO) == 2 && DT % 2 == 0) {
+          // 16-byte stores, half as many store instructions: lane groups lg
+          // and lg^1 trade halves (v_permlane16_swap, as in flush_o).  Every
+          // workgroup ends its items at about the same time, and the 8-byte
+          // stores of O and its residual (32 per wave) held the waves at
+          // issue: HiRes forward -14 us.  (Rows >= N and, without a residual
+          // buffer, the residual stores fall outside their ranges.)
+          const bool res = RES && p.o_res != nullptr;
+          const auto rR = make_rsrc(static_cast<IO*>(RES && p.o_res ? p.o_res : p.o) + (int64_t)plane * N * D,
+                                    res ? (unsigned)N * D * ES : 0u);
+          const int cbase = 4 * (lg & 2);
+#pragma unroll
+          for (int d0 = 0; d0 < DT; d0 += 2) {
+            u32x2 wo[2], wr[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              typedef IO io4 __attribute__((ext_vector_type(4)));
+              io4 a, b;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const float o = oacc[t][d0 + h][r] * inv;
+                a[r] = (IO)o;
+                b[r] = (IO)(o - (float)a[r]);
+              }
+              __builtin_memcpy(&wo[h], &a, 8);
+              __builtin_memcpy(&wr[h], &b, 8);
+            }
+            u32x4 w, x;
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+              const auto r1 = __builtin_amdgcn_permlane16_swap(wo[0][k], wo[1][k], false, false);
+              w[k] = r1[0];
+              w[2 + k] = r1[1];
+              const auto r2 = __builtin_amdgcn_permlane16_swap(wr[0][k], wr[1][k], false, false);
+              x[k] = r2[0];
+              x[2 + k] = r2[1];
+            }
+            const int ch = 16 * (d0 + (lg & 1)) + cbase;
+            buf_store16(w, rO, (unsigned)((row * (int)p.so[2] + ch) * (int)ES), 0u);
+            if constexpr (RES) buf_store16(x, rR, (unsigned)((row * D + ch) * (int)ES), 0u);
+          }
+        } else {
 #pragma unroll
         for (int d = 0; d < DT; ++d) {
           float o4[4];
@@ -1257,6 +1299,7 @@ fwd_kernel(const FwdParams p) {
               buf_store4<IO>(rR, (unsigned)((row * D + 16 * d + 4 * lg) * (int)ES), 0u, r4);
             }
           }
+        }
         }
         const float lse = (m_run[t] + fast_log2(l)) * kLn2;
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(lse), rL, (unsigned)(lg == 0 ? row : N) * 4u, 0u, 0);
