@@ -377,25 +377,52 @@ __global__ void __launch_bounds__(512) bwd_keys_kernel(const BwdParams p) {
   }
 
   // ---- epilogue: lane holds dV / dK-hat of key kv_first + lr, channels 16d + 4lg + (0..3) ----
+  // 16 bytes per lane and store: lane groups lg and lg^1 trade halves
+  // (v_permlane16_swap), so that even lg writes channels 16 d0 + 4 lg .. + 7
+  // and odd lg channels 16 (d0 + 1) + 4 (lg - 1) .. + 7 for d0 = 0, 2, ...;
+  // half the store instructions of 8-byte stores at the tile end, where the
+  // workgroups of a launch round finish together.  Every lane takes part in
+  // the exchange; rows >= N fall outside the descriptors' ranges.
   {
     const int row = kv_first + lr;
-    if (row < N) {
-      IO* __restrict__ dK = const_cast<IO*>(plane_ptr<IO>(p.dk, p.sdk, plane, p.H)) + (int64_t)row * p.sdk[2];
-      IO* __restrict__ dV = const_cast<IO*>(plane_ptr<IO>(p.dv, p.sdv, plane, p.H)) + (int64_t)row * p.sdv[2];
-      // dK-hat = scale * sum (sig dS)(Q-hat c2 fq) / (sig c2 fq)
-      const float ks = p.scale / (sig * c2 * fq);
+    const int trow = min(row, N - 1) + shift;   // (table row of a dropped row: any valid one)
+    const auto rK = make_rsrc(plane_ptr<IO>(p.dk, p.sdk, plane, p.H), (unsigned)(((int64_t)(N - 1) * p.sdk[2] + D) * ES));
+    const auto rV = make_rsrc(plane_ptr<IO>(p.dv, p.sdv, plane, p.H), (unsigned)(((int64_t)(N - 1) * p.sdv[2] + D) * ES));
+    // dK-hat = scale * sum (sig dS)(Q-hat c2 fq) / (sig c2 fq)
+    const float ks = p.scale / (sig * c2 * fq);
+    typedef IO io4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-      for (int d = 0; d < DT; ++d) {
-        float v4[4], g4[4];
+    for (int d0 = 0; d0 < DT; d0 += 2) {
+      u32x2 wv[2], wk[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int d = d0 + h;
+        float g4[4];
+        io4 a, b;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          v4[r] = dvacc[d][r];
+          a[r] = (IO)dvacc[d][r];
           g4[r] = dkacc[d][r] * ks;
         }
-        store4(dV + 16 * d + 4 * lg, 1, true, v4);
-        rope_unrotate4(g4, tab, row + shift, D2, 8 * d + 2 * lg);
-        store4(dK + 16 * d + 4 * lg, 1, true, g4);
+        rope_unrotate4(g4, tab, trow, D2, 8 * d + 2 * lg);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) b[r] = (IO)g4[r];
+        __builtin_memcpy(&wv[h], &a, 8);
+        __builtin_memcpy(&wk[h], &b, 8);
       }
+      u32x4 xv, xk;
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const auto r1 = __builtin_amdgcn_permlane16_swap(wv[0][k], wv[1][k], false, false);
+        xv[k] = r1[0];
+        xv[2 + k] = r1[1];
+        const auto r2 = __builtin_amdgcn_permlane16_swap(wk[0][k], wk[1][k], false, false);
+        xk[k] = r2[0];
+        xk[2 + k] = r2[1];
+      }
+      const int ch = 16 * (d0 + (lg & 1)) + 4 * (lg & 2);
+      buf_store16(xv, rV, (unsigned)((row * (int)p.sdv[2] + ch) * (int)ES), 0u);
+      buf_store16(xk, rK, (unsigned)((row * (int)p.sdk[2] + ch) * (int)ES), 0u);
     }
   }
 }
