@@ -338,20 +338,47 @@ bwd_ds_dq_kernel(const BwdParams p, int n_qt) {
       }
     }
   }
+  // 16 bytes per lane and store: lane groups lg and lg^1 trade halves
+  // (v_permlane16_swap), even lg then holding channels cw + 16 t0 + 4 lg .. + 7
+  // and odd lg channels cw + 16 (t0 + 1) + 4 (lg - 1) .. + 7; half the store
+  // instructions of 8-byte stores.  Every lane takes part in the exchange:
+  // queries >= N (their products were skipped or hold zero rows) fall
+  // outside the descriptor's range, and their table row and dS of the last
+  // key are clamped to query N - 1.
+  {
+    const auto rQ = make_rsrc(dQ, (unsigned)(((int64_t)(N - 1) * p.sdq[2] + D) * sizeof(IO)));
+    typedef IO io4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int q = q0 + qw + 16 * u + lr;
-    if (u < nq && q < N) {
-      const float dl = p.dslast ? p.dslast[prow + q] : 0.f;
+    for (int u = 0; u < 4; ++u) {
+      const int q = q0 + qw + 16 * u + lr;
+      const int qc = min(q, N - 1);
+      const float dl = p.dslast ? p.dslast[prow + qc] : 0.f;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int c = cw + 16 * t + 4 * lg;
-        float g4[4];
+      for (int t0 = 0; t0 < 4; t0 += 2) {
+        u32x2 w[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          g4[i] = p.scale * __builtin_fmaf(dl, kl[t][i], __builtin_ldexpf(acc[t][u][i], emax));
-        rope_unrotate4(g4, tab, q + shift, D2, c / 2);
-        store4(dQ + (int64_t)q * p.sdq[2] + c, 1, true, g4);
+        for (int h = 0; h < 2; ++h) {
+          const int t = t0 + h;
+          const int c = cw + 16 * t + 4 * lg;
+          float g4[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            g4[i] = p.scale * __builtin_fmaf(dl, kl[t][i], __builtin_ldexpf(acc[t][u][i], emax));
+          rope_unrotate4(g4, tab, qc + shift, D2, c / 2);
+          io4 a;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) a[i] = (IO)g4[i];
+          __builtin_memcpy(&w[h], &a, 8);
+        }
+        u32x4 x;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const auto r = __builtin_amdgcn_permlane16_swap(w[0][k], w[1][k], false, false);
+          x[k] = r[0];
+          x[2 + k] = r[1];
+        }
+        const int ch = cw + 16 * (t0 + (lg & 1)) + 4 * (lg & 2);
+        buf_store16(x, rQ, (unsigned)((q * (int)p.sdq[2] + ch) * (int)sizeof(IO)), 0u);
       }
     }
   }
