@@ -91,14 +91,19 @@ int check_ptr(const void* p, int es) {
 // 16-byte vector access: unit d-stride, 16-byte aligned base and strides, a
 // non-negative row stride, and every byte offset inside one (b, h) plane
 // (row n, channel d) below 2^31, so kernels can address a plane as 64-bit
-// base + 32-bit lane offset.
+// base + 32-bit lane offset.  The bound also covers the kRowPad rows past
+// the plane that the kernels address unconditionally (their blocks of up to
+// 256 rows end past N): those offsets must stay below 2^31 too, so that they
+// fall outside the descriptor range (loads read 0, stores are dropped)
+// instead of wrapping around to a row of the plane.
+constexpr int kRowPad = 256;
 int vec_ok(const void* p, const int64_t s[4], int es, int n_rows, int head_dim) {
   if (s[3] != 1) return 0;
   if (reinterpret_cast<uintptr_t>(p) % 16) return 0;
   for (int i = 0; i < 3; ++i)
     if ((s[i] * es) % 16 != 0) return 0;
   if (s[2] < 0) return 0;   // lane offsets are unsigned
-  if ((int64_t)(n_rows - 1) * s[2] + head_dim >= ((int64_t)1 << 31) / es) return 0;
+  if ((int64_t)(n_rows - 1 + kRowPad) * s[2] + head_dim >= ((int64_t)1 << 31) / es) return 0;
   return 1;
 }
 
